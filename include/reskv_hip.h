@@ -1,0 +1,168 @@
+/*
+ * ResKV compressed-KV hot path for AMD Instinct MI355X (gfx950): C ABI.
+ *
+ * Every entry point takes plain device pointers, sizes and a hipStream_t
+ * (passed as void*), enqueues its kernels asynchronously on that stream and
+ * returns 0 on success.  On failure it returns non-zero and
+ * reskv_last_error() describes the problem (thread-local).  No entry point
+ * allocates device memory: outputs and scratch are caller-owned (the Python
+ * layer allocates them with torch).  Shapes use the reference's names:
+ * B batch, H KV heads (H_kv), Hq query heads, T tokens, C centroids, 128 channels.
+ *
+ * Tensor layouts (all contiguous, row-major):
+ *   keys        fp16  [B, H, T, 128]
+ *   centroids   fp16  [B, H, C, 128]
+ *   ids         int32 [B, H, T] (encoders) / int8 [B*H, T] (decode)
+ *   payload     fp16  [B*H, T, nnz] or int32 words (quantised formats)
+ *   metadata    int64 [B*H, T, 2] bitmaps | int32 [B*H, T, 4] tile codes |
+ *               int32 [B*H, T, 2] 2-bit selections
+ *   scale       fp16  [B*H, T]
+ */
+#ifndef RESKV_HIP_H
+#define RESKV_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Thread-local description of the last failure; "" when none. */
+const char* reskv_last_error(void);
+
+/* Library ABI version (bumped on any signature change). */
+int reskv_abi_version(void);
+
+/* ------------------------------------------------------------------ *
+ * Residual encoders (one call encodes one K or V tensor)
+ * ------------------------------------------------------------------ */
+
+/* Tiled / structured-4:16 FP16 encoder.
+ * Replaces ext.compress_fp16 (reskv/csrc/compression.cu:423-473, op bound at :509).
+ * nnz in {16,..,120} divisible by 8 (64: tiled, 32 with struct_index=1: 4:16).
+ * payload fp16 [B,H,T,nnz]; meta int32 [B,H,T,4]. */
+int reskv_compress_fp16(const void* keys, const void* centroids, const int32_t* ids,
+                        void* payload, int32_t* meta, int B, int H, int T, int C,
+                        int nnz, int struct_index, void* stream);
+
+/* Unstructured FP16 encoder (MSB-first int64 bitmaps).
+ * Replaces the PyTorch encoder of reskv/compression.py:75-89 (gather, abs,
+ * topk/sort, scatter, weighted sum).  payload fp16 [B,H,T,nnz];
+ * meta int64 [B,H,T,2]. */
+int reskv_compress_bitmap(const void* keys, const void* centroids, const int32_t* ids,
+                          void* payload, int64_t* meta, int B, int H, int T, int C,
+                          int nnz, void* stream);
+
+/* Unstructured top-nnz + symmetric INT4/INT2 quantiser.
+ * Replaces ext.compress_quantized (reskv/csrc/compression.cu:392-421, op at :510).
+ * qtiles int32 [B,H,T,4*bits]; qscale fp16 [B,H,T]. */
+int reskv_compress_quantized(const void* keys, const void* centroids, const int32_t* ids,
+                             int32_t* qtiles, void* qscale, int B, int H, int T, int C,
+                             int nnz, int bits, void* stream);
+
+/* Structured 1-of-4 INT4 encoder.
+ * Replaces ext.compress_structured_int4 (reskv/csrc/compression.cu:475-504, op at :511).
+ * qpacked int32 [B,H,T,4]; qmeta int32 [B,H,T,2]; qscale fp16 [B,H,T]. */
+int reskv_compress_structured_int4(const void* keys, const void* centroids,
+                                   const int32_t* ids, int32_t* qpacked, int32_t* qmeta,
+                                   void* qscale, int B, int H, int T, int C, void* stream);
+
+/* ------------------------------------------------------------------ *
+ * K-means (Lloyd) over pre-RoPE K or V, one problem per (batch, head)
+ * ------------------------------------------------------------------ */
+
+/* Bytes of scratch reskv_kmeans needs for these sizes. */
+int64_t reskv_kmeans_workspace_bytes(int BH, int T, int C);
+
+/* Lloyd iterations with centres initialised by the caller.
+ * Replaces the torch loop of reskv/compression.py:37-53 (cdist, argmin,
+ * one_hot, bmm).  x fp16 [BH,T,128]; centers_init fp32 [BH,C,128] (the
+ * linspace-selected tokens); centers_out fp16 [BH,C,128]; ids int32 [BH,T]
+ * (from the last assignment).  value_mode=0: K semantics (empty cluster keeps
+ * its centre); 1: V semantics (empty cluster -> 0). */
+int reskv_kmeans(const void* x, const float* centers_init, void* centers_out, int32_t* ids,
+                 int BH, int T, int C, int iterations, int value_mode, void* workspace,
+                 int64_t workspace_bytes, void* stream);
+
+/* Assignment step only: ids = argmin_c |x - c|^2 (lowest index on ties).
+ * Replaces the assignment of reskv/compression.py:61-69 (_incremental_cluster,
+ * one decode group against the shared centroid table).  centers fp32 [BH,C,128];
+ * workspace as for reskv_kmeans. */
+int reskv_kmeans_assign(const void* x, const float* centers, int32_t* ids, int BH, int T, int C,
+                        void* workspace, int64_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------ *
+ * Split-K fused decode attention over the compressed cache
+ * ------------------------------------------------------------------ */
+
+/* Residual formats of one compressed tensor. */
+enum reskv_format {
+    RESKV_FMT_BITMAP = 0,      /* fp16 payload [nnz] + int64[2] MSB-first bitmap   */
+    RESKV_FMT_TILED = 1,       /* fp16 payload [nnz] + int32[4] 16-bit tile masks  */
+    RESKV_FMT_STRUCT16 = 2,    /* fp16 payload [32]  + int32[4] 4:16 nibble codes  */
+    RESKV_FMT_STRUCT_INT4 = 3, /* int32 payload [4]  + int32[2] 2-bit codes + scale */
+    RESKV_FMT_QUANT = 4        /* int32 payload [4*bits] signed codes + scale       */
+};
+
+/* One compressed tensor as the decode kernels read it. */
+typedef struct reskv_ctensor {
+    const void* centroids;   /* fp16 [B*H, nc, 128] */
+    const int8_t* ids;       /* int8 [B*H, T] */
+    const void* payload;     /* fp16 or int32 words [B*H, T, width] */
+    const void* meta;        /* metadata words or NULL */
+    const void* scale;       /* fp16 [B*H, T] or NULL */
+    int nc;                  /* centroids per head (1..64) */
+    int format;              /* enum reskv_format */
+    int width;               /* payload last-dim width (values or words) */
+    int bits;                /* 16, 4 or 2 */
+} reskv_ctensor;
+
+/* Bytes of split-K scratch reskv_decode needs; splits<=0 means automatic. */
+int64_t reskv_decode_workspace_bytes(int B, int Hq, int H, int T, int splits);
+
+/* Split count reskv_decode will use for these sizes (splits<=0: automatic,
+ * chosen from the 256-CU occupancy; >0: min(splits, T)). */
+int reskv_decode_splits(int B, int Hq, int H, int T, int splits);
+
+/* Decode one query token per (batch, query head) against the compressed cache.
+ * Replaces the deferred ops ext.decode_fp16 / decode_structured_fp16 /
+ * decode_structured_int4 (reskv/csrc/cluster_mass.cu:1177-1459, ops at
+ * :1512-1515) and the per-token ops ext.decode_fp16 / decode_int4 /
+ * decode_quantized (reskv/csrc/attention.cu:665-835, 1296-1348, ops at
+ * :1350-1354).  q fp16 [B*Hq,128] (pre-RoPE); inv_freq fp32 [64];
+ * out fp16 [B*Hq,128] (normalised); m, l fp32 [B*Hq] (max score and
+ * sum of exp(score - m)); either of m, l may be NULL. */
+int reskv_decode(const void* q, const reskv_ctensor* k, const reskv_ctensor* v,
+                 const float* inv_freq, int B, int Hq, int H, int T, int start_pos,
+                 int pos_q, float scaling, int splits, void* out, float* m, float* l,
+                 void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Joint softmax of the compressed result with precomputed fp32 recent scores.
+ * Replaces the deferred ext.merge_recent (reskv/csrc/cluster_mass.cu:1461-1508,
+ * op at :1515).  comp_out fp16 [B*Hq,128]; comp_m, comp_l fp32 [B*Hq];
+ * scores fp32 [B,Hq,Tr]; v_recent fp16 [B,H,Tr,128]; out fp16 [B*Hq,128]. */
+int reskv_merge_recent_scores(const void* comp_out, const float* comp_m, const float* comp_l,
+                              const float* scores, const void* v_recent, int B, int Hq,
+                              int H, int Tr, void* out, void* stream);
+
+/* Joint softmax of the compressed result with dense rotated recent tokens.
+ * Replaces the per-token ext.merge_recent (reskv/csrc/attention.cu:839-906,
+ * op at :1355).  q_rope fp16 [B*Hq,128]; k_recent, v_recent fp16 [B,H,Tr,128]. */
+int reskv_merge_recent_qk(const void* comp_out, const float* comp_m, const float* comp_l,
+                          const void* q_rope, const void* k_recent, const void* v_recent,
+                          int B, int Hq, int H, int Tr, float scaling, void* out,
+                          void* stream);
+
+/* Dense fp16 decode attention (the uncompressed baseline at the same shapes):
+ * q fp16 [B*Hq,128] pre-RoPE, k fp16 [B,H,T,128] pre-RoPE, v fp16 [B,H,T,128].
+ * Same split-K engine and RoPE as reskv_decode, out fp16 [B*Hq,128]. */
+int reskv_decode_dense(const void* q, const void* k, const void* v, const float* inv_freq,
+                       int B, int Hq, int H, int T, int start_pos, int pos_q, float scaling,
+                       int splits, void* out, float* m, float* l, void* workspace,
+                       int64_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RESKV_HIP_H */

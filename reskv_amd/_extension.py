@@ -1,0 +1,386 @@
+"""Native operator families behind the reference's loader interface.
+
+``load_extension(family, plan=None, device_index=0)`` keeps the signature,
+caching and family names of ``reskv/_extension.py:14-61`` and returns a
+namespace whose attributes are the same operators with the same argument
+order (``reskv/csrc/compression.cu:508-512``, ``attention.cu:1350-1355``,
+``cluster_mass.cu:1511-1516``).  Behind them is the prebuilt gfx950 library
+``libreskv_hip.so`` (C ABI, ``include/reskv_hip.h``) instead of a JIT-built
+CUDA extension; plan fields select formats at run time instead of ``-D``
+rebuilds.
+
+Each operator validates like the reference's ``TORCH_CHECK`` (raising
+``RuntimeError``), allocates its outputs and split-K scratch with torch on
+the input's device, and enqueues the kernels on torch's current stream of
+that device without synchronising.
+"""
+
+from functools import lru_cache
+from types import SimpleNamespace
+
+import torch
+
+from . import _lib
+from .config import KernelPlan
+
+FAMILIES = ("compression", "attention", "cluster_mass")
+
+
+# ---------------------------------------------------------------------------
+# small helpers
+# ---------------------------------------------------------------------------
+
+def _require(cond, msg):
+    if not cond:
+        raise RuntimeError(msg)
+
+
+def _ptr(t):
+    return None if t is None or t.numel() == 0 else t.data_ptr()
+
+
+def _stream(device):
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _dev_check(*tensors):
+    dev = tensors[0].device
+    for t in tensors:
+        if t is not None and t.numel() > 0:
+            _require(t.is_cuda and t.device == dev, "all tensors must be on the same GPU")
+            _require(t.is_contiguous(), "tensors must be contiguous")
+    return dev
+
+
+def _empty(shape, dtype, device):
+    return torch.empty(shape, dtype=dtype, device=device)
+
+
+def _workspace(nbytes, device):
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+
+
+def _frequencies(inv_freq, rope_base, device):
+    """The 64 RoPE frequencies: the caller's, or theta-derived (reskv/reference.py:73-77)."""
+    if inv_freq is not None and inv_freq.numel():
+        _require(inv_freq.numel() == 64 and inv_freq.dtype == torch.float32, "inv_freq must be fp32 [64]")
+        return inv_freq.to(device).contiguous()
+    idx = torch.arange(64, device=device).float()
+    return (float(rope_base) ** (-idx / 64)).float().contiguous()
+
+
+# ---------------------------------------------------------------------------
+# compression family
+# ---------------------------------------------------------------------------
+
+def _check_encoder_inputs(keys, centroids, cluster_ids):
+    _require(keys.is_cuda and centroids.is_cuda and cluster_ids.is_cuda, "inputs must be CUDA tensors")
+    _require(keys.dtype == torch.float16 and centroids.dtype == torch.float16, "keys and centroids must be float16")
+    _require(cluster_ids.dtype == torch.int32, "cluster_ids must be int32")
+    _require(keys.dim() == 4 and centroids.dim() == 4 and cluster_ids.dim() == 3,
+             "expected keys[B,nh,T,D], centroids[B,nh,C,D], cluster_ids[B,nh,T]")
+    _require(keys.shape[3] == 128 and centroids.shape[3] == 128, "Only D=128 is supported")
+    _require(tuple(cluster_ids.shape) == tuple(keys.shape[:3]) and centroids.shape[:2] == keys.shape[:2],
+             "keys, centroids and cluster_ids disagree in [B, nh, T]")
+    _dev_check(keys, centroids, cluster_ids)
+    b, h, t, _ = keys.shape
+    return b, h, t, centroids.shape[2]
+
+
+def compress_fp16(keys, centroids, cluster_ids, nnz_per_token, use_4x16_struct_index):
+    """Tiled / structured-4:16 FP16 encoder (reskv/csrc/compression.cu:423-473)."""
+    b, h, t, c = _check_encoder_inputs(keys, centroids, cluster_ids)
+    nnz = int(nnz_per_token)
+    dev = keys.device
+    payload = _empty((b, h, t, nnz), torch.float16, dev)
+    meta = _empty((b, h, t, 4), torch.int32, dev)
+    with torch.cuda.device(dev):
+        _lib.check(_lib.lib().reskv_compress_fp16(
+            keys.data_ptr(), centroids.data_ptr(), cluster_ids.data_ptr(), payload.data_ptr(), meta.data_ptr(),
+            b, h, t, c, nnz, int(bool(use_4x16_struct_index)), _stream(dev)), "compress_fp16")
+    return [payload, meta]
+
+
+def compress_bitmap(keys, centroids, cluster_ids, nnz_per_token):
+    """Unstructured FP16 encoder with MSB-first int64 bitmaps (reskv/compression.py:75-89)."""
+    b, h, t, c = _check_encoder_inputs(keys, centroids, cluster_ids)
+    nnz = int(nnz_per_token)
+    dev = keys.device
+    payload = _empty((b, h, t, nnz), torch.float16, dev)
+    meta = _empty((b, h, t, 2), torch.int64, dev)
+    with torch.cuda.device(dev):
+        _lib.check(_lib.lib().reskv_compress_bitmap(
+            keys.data_ptr(), centroids.data_ptr(), cluster_ids.data_ptr(), payload.data_ptr(), meta.data_ptr(),
+            b, h, t, c, nnz, _stream(dev)), "compress_bitmap")
+    return [payload, meta]
+
+
+def compress_quantized(keys, centroids, cluster_ids, nnz_per_token, bitwidth):
+    """Unstructured top-nnz + signed INT4/INT2 (reskv/csrc/compression.cu:392-421)."""
+    b, h, t, c = _check_encoder_inputs(keys, centroids, cluster_ids)
+    bits = int(bitwidth)
+    dev = keys.device
+    qtiles = _empty((b, h, t, 4 * bits), torch.int32, dev)
+    qscale = _empty((b, h, t), torch.float16, dev)
+    with torch.cuda.device(dev):
+        _lib.check(_lib.lib().reskv_compress_quantized(
+            keys.data_ptr(), centroids.data_ptr(), cluster_ids.data_ptr(), qtiles.data_ptr(), qscale.data_ptr(),
+            b, h, t, c, int(nnz_per_token), bits, _stream(dev)), "compress_quantized")
+    return [qtiles, qscale]
+
+
+def compress_structured_int4(keys, centroids, cluster_ids):
+    """Structured 1-of-4 INT4 encoder (reskv/csrc/compression.cu:475-504)."""
+    b, h, t, c = _check_encoder_inputs(keys, centroids, cluster_ids)
+    dev = keys.device
+    qpacked = _empty((b, h, t, 4), torch.int32, dev)
+    qmeta = _empty((b, h, t, 2), torch.int32, dev)
+    qscale = _empty((b, h, t), torch.float16, dev)
+    with torch.cuda.device(dev):
+        _lib.check(_lib.lib().reskv_compress_structured_int4(
+            keys.data_ptr(), centroids.data_ptr(), cluster_ids.data_ptr(), qpacked.data_ptr(), qmeta.data_ptr(),
+            qscale.data_ptr(), b, h, t, c, _stream(dev)), "compress_structured_int4")
+    return [qpacked, qmeta, qscale]
+
+
+def kmeans(x, centers_init, iterations, value):
+    """Lloyd k-means (reskv/compression.py:37-53) from caller-chosen initial centres.
+
+    x fp16 [BH, T, 128]; centers_init fp32 [BH, C, 128].
+    Returns (centres fp16 [BH, C, 128], ids int32 [BH, T]).
+    """
+    _require(x.dtype == torch.float16 and x.dim() == 3 and x.shape[2] == 128, "x must be fp16 [BH,T,128]")
+    _require(centers_init.dtype == torch.float32 and centers_init.dim() == 3, "centres must be fp32 [BH,C,128]")
+    dev = _dev_check(x, centers_init)
+    bh, t, _ = x.shape
+    c = centers_init.shape[1]
+    out = _empty((bh, c, 128), torch.float16, dev)
+    ids = _empty((bh, t), torch.int32, dev)
+    L = _lib.lib()
+    ws = _workspace(L.reskv_kmeans_workspace_bytes(bh, t, c), dev)
+    with torch.cuda.device(dev):
+        _lib.check(L.reskv_kmeans(x.data_ptr(), centers_init.data_ptr(), out.data_ptr(), ids.data_ptr(), bh, t, c,
+                                  int(iterations), int(bool(value)), ws.data_ptr(), ws.numel(), _stream(dev)),
+                   "kmeans")
+    return out, ids
+
+
+def kmeans_assign(x, centers):
+    """Nearest-centre ids, lowest index on ties. x fp16 [BH,T,128]; centres fp32 [BH,C,128]."""
+    _require(x.dtype == torch.float16 and x.dim() == 3 and x.shape[2] == 128, "x must be fp16 [BH,T,128]")
+    _require(centers.dtype == torch.float32 and centers.dim() == 3, "centres must be fp32 [BH,C,128]")
+    dev = _dev_check(x, centers)
+    bh, t, _ = x.shape
+    c = centers.shape[1]
+    ids = _empty((bh, t), torch.int32, dev)
+    L = _lib.lib()
+    ws = _workspace(L.reskv_kmeans_workspace_bytes(bh, t, c), dev)
+    with torch.cuda.device(dev):
+        _lib.check(L.reskv_kmeans_assign(x.data_ptr(), centers.data_ptr(), ids.data_ptr(), bh, t, c,
+                                         ws.data_ptr(), ws.numel(), _stream(dev)), "kmeans_assign")
+    return ids
+
+
+# ---------------------------------------------------------------------------
+# decode families
+# ---------------------------------------------------------------------------
+
+def _ctensor(cent, ids, payload, meta, scale, fmt, bits):
+    _require(cent.dtype == torch.float16 and cent.dim() == 3 and cent.shape[2] == 128,
+             "centroids must be fp16 [B*nh_kv, nc, 128]")
+    _require(ids.dtype == torch.int8 and ids.dim() == 2, "cluster ids must be int8 [B*nh_kv, T]")
+    _require(payload.dim() == 3 and payload.shape[:2] == ids.shape, "payload must be [B*nh_kv, T, width]")
+    _require(cent.shape[0] == ids.shape[0], "centroid batch-head mismatch")
+    if meta is not None and meta.numel():
+        _require(meta.dim() == 3 and meta.shape[:2] == ids.shape, "metadata shape mismatch")
+    if scale is not None and scale.numel():
+        _require(scale.dtype == torch.float16 and tuple(scale.shape) == tuple(ids.shape), "scale shape mismatch")
+    return _lib.CTensor(_ptr(cent), _ptr(ids), _ptr(payload), _ptr(meta), _ptr(scale), int(cent.shape[1]),
+                        int(fmt), int(payload.shape[2]), int(bits))
+
+
+def _decode(Q, kdesc, vdesc, keep, nh_kv, nh, start_pos, pos_q, rope_base, scaling, splits, inv_freq,
+            return_stats=True):
+    _require(Q.is_cuda and Q.dtype == torch.float16, "Q must be fp16 CUDA")
+    _require(Q.dim() == 2 and Q.shape[1] == 128, "Q must be [B*nh, 128]")
+    _dev_check(Q, *keep)
+    nh_kv, nh = int(nh_kv), int(nh)
+    _require(nh % nh_kv == 0, "num_q_heads must be divisible by num_kv_heads")
+    _require(nh // nh_kv in (1, 2, 4, 8), "supported GQA ratios are 1, 2, 4 and 8")
+    bnh = Q.shape[0]
+    _require(bnh % nh == 0, "Q rows must be a multiple of num_q_heads")
+    b = bnh // nh
+    ids = keep[1]
+    _require(ids.shape[0] == b * nh_kv, "cache batch-head count does not match Q")
+    t = ids.shape[1]
+    dev = Q.device
+    freq = _frequencies(inv_freq, rope_base, dev)
+    L = _lib.lib()
+    out = _empty((bnh, 128), torch.float16, dev)
+    m = _empty((bnh,), torch.float32, dev)
+    l = _empty((bnh,), torch.float32, dev)
+    ws = _workspace(L.reskv_decode_workspace_bytes(b, nh, nh_kv, t, int(splits)), dev)
+    with torch.cuda.device(dev):
+        _lib.check(L.reskv_decode(Q.data_ptr(), kdesc, vdesc, freq.data_ptr(), b, nh, nh_kv, t, int(start_pos),
+                                  int(pos_q), float(scaling), int(splits), out.data_ptr(), m.data_ptr(),
+                                  l.data_ptr(), ws.data_ptr(), ws.numel(), _stream(dev)), "decode")
+    return [out, m, l] if return_stats else [out]
+
+
+def _make_cluster_mass():
+    def decode_fp16(Q, kc, ki, kp, kbitmap, vc, vi, vp, vbitmap, nh_kv, nh, start_pos, pos_q, rope_base,
+                    scaling, return_stats, splits, inv_freq):
+        """Deferred unstructured FP16 decode (reskv/csrc/cluster_mass.cu:1177-1296)."""
+        for t, name in ((kp, "k_sparse"), (vp, "v_sparse")):
+            _require(t.dtype == torch.float16, f"cmass fp16 sparse-only: {name} must be fp16")
+        for t in (kbitmap, vbitmap):
+            _require(t.dtype == torch.int64 and t.shape[-1] == 2, "bitmaps must be int64 [B*nh_kv, T, 2]")
+        kd = _ctensor(kc, ki, kp, kbitmap, None, _lib.FMT_BITMAP, 16)
+        vd = _ctensor(vc, vi, vp, vbitmap, None, _lib.FMT_BITMAP, 16)
+        return _decode(Q, kd, vd, (kc, ki, kp, kbitmap, vc, vi, vp, vbitmap), nh_kv, nh, start_pos, pos_q,
+                       rope_base, scaling, splits, inv_freq, bool(return_stats))
+
+    def _structured(int4):
+        def op(Q, kc, ki, kqv, kmeta, kscale, vc, vi, vqv, vmeta, vscale, nh_kv, nh, start_pos, pos_q, rope_base,
+               scaling, return_stats, splits, inv_freq):
+            want = torch.int32 if int4 else torch.float16
+            _require(kqv.dtype == want and vqv.dtype == want, "structured payload dtype mismatch")
+            _require(kmeta.dtype == torch.int32 and vmeta.dtype == torch.int32, "structured metadata must be int32")
+            _require(kmeta.shape[-1] == (2 if int4 else 4) and vmeta.shape[-1] == (2 if int4 else 4),
+                     "structured metadata width mismatch")
+            _require(kqv.shape[-1] == (4 if int4 else 32) and vqv.shape[-1] == (4 if int4 else 32),
+                     "4:16 structured payload width mismatch")
+            fmt = _lib.FMT_STRUCT_INT4 if int4 else _lib.FMT_STRUCT16
+            bits = 4 if int4 else 16
+            ks = kscale if int4 else None
+            vs = vscale if int4 else None
+            if int4:
+                _require(ks is not None and ks.numel() and vs is not None and vs.numel(),
+                         "INT4 structured scales must be fp16")
+            kd = _ctensor(kc, ki, kqv, kmeta, ks, fmt, bits)
+            vd = _ctensor(vc, vi, vqv, vmeta, vs, fmt, bits)
+            keep = (kc, ki, kqv, kmeta, vc, vi, vqv, vmeta) + ((ks, vs) if int4 else ())
+            return _decode(Q, kd, vd, keep, nh_kv, nh, start_pos, pos_q, rope_base, scaling, splits, inv_freq,
+                           bool(return_stats))
+
+        op.__doc__ = ("Deferred structured %s decode (reskv/csrc/cluster_mass.cu:1298-1459)."
+                      % ("INT4" if int4 else "FP16"))
+        return op
+
+    def merge_recent(comp_out, comp_m, comp_l, scores_recent, v_recent, nh_kv, nh):
+        """Joint softmax with precomputed fp32 recent scores (reskv/csrc/cluster_mass.cu:1461-1508)."""
+        _require(comp_out.dim() == 2 and comp_out.shape[1] == 128, "comp_out must be [B*nh, 128]")
+        nh_kv, nh = int(nh_kv), int(nh)
+        _require(nh % nh_kv == 0, "num_q_heads must be divisible by num_kv_heads")
+        _require(scores_recent.dtype == torch.float32 and scores_recent.dim() == 3, "scores must be fp32 [B,nh,Tr]")
+        _require(v_recent.dtype == torch.float16 and v_recent.dim() == 4, "v_recent must be fp16 [B,nh_kv,Tr,128]")
+        dev = _dev_check(comp_out, comp_m, comp_l, scores_recent, v_recent)
+        b = comp_out.shape[0] // nh
+        tr = scores_recent.shape[2]
+        out = torch.empty_like(comp_out)
+        with torch.cuda.device(dev):
+            _lib.check(_lib.lib().reskv_merge_recent_scores(
+                comp_out.data_ptr(), comp_m.data_ptr(), comp_l.data_ptr(), _ptr(scores_recent), _ptr(v_recent),
+                b, nh, nh_kv, tr, out.data_ptr(), _stream(dev)), "merge_recent")
+        return out
+
+    return SimpleNamespace(decode_fp16=decode_fp16, decode_structured_fp16=_structured(False),
+                           decode_structured_int4=_structured(True), merge_recent=merge_recent)
+
+
+def _make_attention(plan):
+    struct_index = plan is not None and plan.layout == "structured"
+
+    def _per_token(int4):
+        def op(Q, kc, ki, kp, km, ks, vc, vi, vp, vm, vs, nh_kv, nh, start_pos, pos_q, rope_base, scaling, splits,
+               inv_freq):
+            want = torch.int32 if int4 else torch.float16
+            _require(kp.dtype == want and vp.dtype == want, "payload dtype mismatch")
+            _require(km.dtype == torch.int32 and vm.dtype == torch.int32, "k_qmeta/v_qmeta must be int32")
+            if int4:
+                fmt, bits = _lib.FMT_STRUCT_INT4, 4
+                _require(ks is not None and ks.numel() and vs is not None and vs.numel(), "INT4 scales must be fp16")
+            else:
+                fmt = _lib.FMT_STRUCT16 if struct_index else _lib.FMT_TILED
+                bits, ks, vs = 16, None, None
+            kd = _ctensor(kc, ki, kp, km, ks, fmt, bits)
+            vd = _ctensor(vc, vi, vp, vm, vs, fmt, bits)
+            keep = (kc, ki, kp, km, vc, vi, vp, vm) + ((ks, vs) if int4 else ())
+            return _decode(Q, kd, vd, keep, nh_kv, nh, start_pos, pos_q, rope_base, scaling, splits, inv_freq)
+
+        op.__doc__ = "Per-token %s decode (reskv/csrc/attention.cu:665-835)." % ("INT4" if int4 else "FP16")
+        return op
+
+    def decode_quantized(Q, kc, ki, kp, ks, vc, vi, vp, vs, nh_kv, nh, start_pos, pos_q, rope_base, scaling,
+                         k_bits, v_bits, splits, inv_freq):
+        """Per-token unstructured INT4/INT2 decode (reskv/csrc/attention.cu:1296-1348)."""
+        _require(kp.dtype == torch.int32 and vp.dtype == torch.int32, "quantized payloads must be int32")
+        _require(int(k_bits) in (2, 4) and int(v_bits) in (2, 4), "bit widths must be 2 or 4")
+        kd = _ctensor(kc, ki, kp, None, ks, _lib.FMT_QUANT, int(k_bits))
+        vd = _ctensor(vc, vi, vp, None, vs, _lib.FMT_QUANT, int(v_bits))
+        return _decode(Q, kd, vd, (kc, ki, kp, ks, vc, vi, vp, vs), nh_kv, nh, start_pos, pos_q, rope_base,
+                       scaling, splits, inv_freq)
+
+    def merge_recent(comp_out, comp_m, comp_l, Q_rope, k_recent, v_recent, nh_kv, nh, scaling):
+        """Joint softmax with dense rotated recent tokens (reskv/csrc/attention.cu:839-906)."""
+        _require(comp_out.dim() == 2 and comp_out.shape[1] == 128, "comp_out must be [B*nh, 128]")
+        nh_kv, nh = int(nh_kv), int(nh)
+        _require(nh % nh_kv == 0, "num_q_heads must be divisible by num_kv_heads")
+        _require(k_recent.dim() == 4 and k_recent.shape == v_recent.shape, "recent K/V must be [B,nh_kv,Tr,128]")
+        dev = _dev_check(comp_out, comp_m, comp_l, Q_rope, k_recent, v_recent)
+        b = comp_out.shape[0] // nh
+        tr = k_recent.shape[2]
+        out = torch.empty_like(comp_out)
+        with torch.cuda.device(dev):
+            _lib.check(_lib.lib().reskv_merge_recent_qk(
+                comp_out.data_ptr(), comp_m.data_ptr(), comp_l.data_ptr(), _ptr(Q_rope), _ptr(k_recent),
+                _ptr(v_recent), b, nh, nh_kv, tr, float(scaling), out.data_ptr(), _stream(dev)), "merge_recent")
+        return out
+
+    return SimpleNamespace(decode_fp16=_per_token(False), decode_int4=_per_token(True),
+                           decode_quantized=decode_quantized, merge_recent=merge_recent)
+
+
+def _make_compression():
+    return SimpleNamespace(compress_fp16=compress_fp16, compress_quantized=compress_quantized,
+                           compress_structured_int4=compress_structured_int4, compress_bitmap=compress_bitmap,
+                           kmeans=kmeans, kmeans_assign=kmeans_assign)
+
+
+@lru_cache(maxsize=32)
+def load_extension(family: str, plan: KernelPlan | None = None, device_index: int = 0):
+    """Operator namespace for ``family`` (reskv/_extension.py:14-61).
+
+    Raises ValueError for an unknown family and RuntimeError when the HIP
+    library is unavailable; there is no CPU fallback.
+    """
+    if family not in FAMILIES:
+        raise ValueError(f"unknown native family: {family}")
+    _lib.lib()
+    if family == "compression":
+        return _make_compression()
+    if family == "attention":
+        return _make_attention(plan)
+    return _make_cluster_mass()
+
+
+def dense_decode(q, k, v, inv_freq, *, position, start_position=0, scaling=None, splits=0):
+    """Dense fp16 decode attention baseline on the same split-K engine.
+
+    q fp16 [B, Hq, 1, 128] pre-RoPE; k, v fp16 [B, H, T, 128] (k pre-RoPE).
+    Returns fp16 [B, Hq, 1, 128].
+    """
+    _require(q.dtype == torch.float16 and k.dtype == torch.float16 and v.dtype == torch.float16, "fp16 inputs")
+    dev = _dev_check(q, k, v)
+    b, hq = q.shape[:2]
+    h, t = k.shape[1], k.shape[2]
+    scale = 128 ** -0.5 if scaling is None else float(scaling)
+    freq = _frequencies(inv_freq, 500000.0, dev)
+    L = _lib.lib()
+    out = _empty((b * hq, 128), torch.float16, dev)
+    ws = _workspace(L.reskv_decode_workspace_bytes(b, hq, h, t, int(splits)), dev)
+    with torch.cuda.device(dev):
+        _lib.check(L.reskv_decode_dense(q.data_ptr(), k.data_ptr(), v.data_ptr(), freq.data_ptr(), b, hq, h, t,
+                                        int(start_position), int(position), scale, int(splits), out.data_ptr(),
+                                        None, None, ws.data_ptr(), ws.numel(), _stream(dev)), "decode_dense")
+    return out.reshape(b, hq, 1, 128)

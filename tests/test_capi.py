@@ -1,0 +1,103 @@
+"""The C-ABI library: loads on a CPU-only host, exports every declared symbol,
+and rejects bad arguments before touching a GPU (no compute calls here)."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from reskv_amd import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "reskv_hip.h"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\**\s+\**(reskv_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_header_declares_the_operator_surface():
+    names = declared_functions()
+    for required in ("reskv_compress_fp16", "reskv_compress_bitmap", "reskv_compress_quantized",
+                     "reskv_compress_structured_int4", "reskv_kmeans", "reskv_kmeans_assign", "reskv_decode",
+                     "reskv_merge_recent_scores", "reskv_merge_recent_qk", "reskv_decode_dense"):
+        assert required in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.lib()
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+        assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
+    assert lib.reskv_abi_version() == 1
+
+
+def _err(status):
+    assert status != 0
+    return _lib.lib().reskv_last_error().decode()
+
+
+def test_null_pointers_are_rejected_without_a_gpu():
+    lib = _lib.lib()
+    assert "null" in _err(lib.reskv_compress_fp16(None, None, None, None, None, 1, 1, 1, 1, 32, 1, None))
+    assert "null" in _err(lib.reskv_compress_bitmap(None, None, None, None, None, 1, 1, 1, 1, 32, None))
+    assert "null" in _err(lib.reskv_kmeans(None, None, None, None, 1, 1, 1, 1, 0, None, 0, None))
+    assert "null" in _err(lib.reskv_merge_recent_qk(None, None, None, None, None, None, 1, 4, 1, 1, 1.0, None,
+                                                    None))
+
+
+@pytest.mark.parametrize(
+    "args,message",
+    [
+        (dict(nnz=30, struct_index=0), "divisible by 8"),
+        (dict(nnz=64, struct_index=1), "4:16"),
+        (dict(C=65), "centroid count"),
+        (dict(T=0), "positive"),
+    ],
+)
+def test_encoder_argument_checks(args, message):
+    lib = _lib.lib()
+    p = ctypes.c_void_p(16)  # never dereferenced: validation fails first
+    kw = dict(B=1, H=1, T=4, C=4, nnz=32, struct_index=1)
+    kw.update(args)
+    st = lib.reskv_compress_fp16(p, p, p, p, p, kw["B"], kw["H"], kw["T"], kw["C"], kw["nnz"],
+                                 kw["struct_index"], None)
+    assert message in _err(st)
+
+
+def test_quantiser_argument_checks():
+    lib = _lib.lib()
+    p = ctypes.c_void_p(16)
+    assert "bits" in _err(lib.reskv_compress_quantized(p, p, p, p, p, 1, 1, 4, 4, 64, 3, None))
+    assert "nnz" in _err(lib.reskv_compress_quantized(p, p, p, p, p, 1, 1, 4, 4, 48, 4, None))
+
+
+def test_decode_descriptor_checks():
+    lib = _lib.lib()
+    p = ctypes.c_void_p(16)
+    good = _lib.CTensor(p, p, p, p, None, 32, _lib.FMT_BITMAP, 64, 16)
+    bad_fmt = _lib.CTensor(p, p, p, p, None, 32, 9, 64, 16)
+    bad_nc = _lib.CTensor(p, p, p, p, None, 65, _lib.FMT_BITMAP, 64, 16)
+    bad_quant = _lib.CTensor(p, p, p, None, None, 32, _lib.FMT_QUANT, 16, 4)
+    for desc, msg in ((bad_fmt, "unknown residual format"), (bad_nc, "centroid count"), (bad_quant, "quantised")):
+        st = lib.reskv_decode(p, ctypes.byref(desc), ctypes.byref(good), p, 1, 32, 8, 16, 0, 16, 0.1, 0, p, None,
+                              None, p, 1 << 30, None)
+        assert msg in _err(st)
+    st = lib.reskv_decode(p, ctypes.byref(good), ctypes.byref(good), p, 1, 24, 8, 16, 0, 16, 0.1, 0, p, None, None,
+                          p, 1 << 30, None)
+    assert "GQA" in _err(st)
+    st = lib.reskv_decode(p, ctypes.byref(good), ctypes.byref(good), p, 1, 32, 8, 16, 0, 16, 0.1, 0, p, None, None,
+                          p, 16, None)
+    assert "workspace" in _err(st)
+
+
+def test_split_and_workspace_sizing():
+    lib = _lib.lib()
+    for b in (1, 4, 8, 16, 32):
+        s = lib.reskv_decode_splits(b, 32, 8, 8192, 0)
+        assert 1 <= s <= 256
+        assert lib.reskv_decode_workspace_bytes(b, 32, 8, 8192, 0) == b * 32 * s * (2 + 128 + 64) * 4
+    assert lib.reskv_decode_splits(1, 32, 8, 5, 20) == 5  # explicit split counts are capped at T
+    assert lib.reskv_decode_splits(1, 32, 8, 8192, 20) == 20
+    assert lib.reskv_kmeans_workspace_bytes(16, 8192, 32) > 0

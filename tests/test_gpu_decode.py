@@ -1,0 +1,195 @@
+"""Split-K fused decode (HIP) vs the float64 oracle, through reskv_amd.attention.
+
+The case matrix follows reskv tests/test_cuda.py: every bits x sparsity x
+layout x fusion combination with and without a dense recent window, GQA 1/8
+with 64 centroids and a start offset, large logits, large finite recent
+scores, theta-derived RoPE, non-default streams; plus config-0-distributed K
+(outlier channels) at T = 1024 and the split-merge invariance.
+Tolerance: max-abs <= 2e-3 on the fp16 output.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import reskv_oracle as o
+from reskv_amd import ResKVKernelConfig, attention, compress
+from tests.gpu_helpers import ATOL, expected_attention, np_, outlier_kv, reference_test_inputs, theta_freq
+
+pytestmark = pytest.mark.gpu
+
+CASES = [
+    (16, 0.5, "tiled", "per_token"),
+    (16, 0.5, "unstructured", "deferred"),
+    (16, 0.75, "unstructured", "deferred"),
+    (16, 0.75, "structured", "per_token"),
+    (16, 0.75, "structured", "deferred"),
+    (4, 0.5, "unstructured", "per_token"),
+    (4, 0.75, "unstructured", "per_token"),
+    (4, 0.75, "structured", "per_token"),
+    (4, 0.75, "structured", "deferred"),
+    (2, 0.5, "unstructured", "per_token"),
+    (2, 0.75, "unstructured", "per_token"),
+]
+
+
+def _max_err(out, ref):
+    return float(np.abs(np_(out).astype(np.float64) - ref).max())
+
+
+@pytest.mark.parametrize("bits,sparsity,layout,fusion", CASES)
+def test_fused_and_mixed_against_oracle(device, bits, sparsity, layout, fusion):
+    k, v, q, clustering = reference_test_inputs()
+    cfg = ResKVKernelConfig(bits=bits, sparsity=sparsity, layout=layout, centroid_fusion=fusion)
+    cache = compress(k, v, cfg, clustering=clustering)
+    freq = theta_freq() / torch.linspace(1, 8, 64, device=device)  # catches a hard-coded theta
+    out = attention(q, cache, position=288, inv_freq=freq)
+    assert _max_err(out, expected_attention(q, cache, position=288, inv_freq=freq)) <= ATOL
+    g = torch.Generator().manual_seed(5)
+    kr = (torch.randn(1, 1, 32, 128, generator=g) * 0.5).half().to(device)
+    vr = (torch.randn(1, 1, 32, 128, generator=g) * 0.5).half().to(device)
+    qr = torch.from_numpy(o.rotate(np_(q).astype(np.float64), np.array([288]), np_(freq))).half().to(device)
+    mixed = attention(q, cache, position=288, inv_freq=freq, recent=(qr, kr, vr))
+    ref = expected_attention(q, cache, position=288, inv_freq=freq, recent=(qr, kr, vr))
+    assert _max_err(mixed, ref) <= ATOL
+
+
+@pytest.mark.parametrize("bits,layout", [(16, "unstructured"), (16, "structured"), (4, "unstructured"),
+                                         (4, "structured"), (2, "unstructured")])
+def test_current_stream(device, bits, layout):
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        k, v, q, c = reference_test_inputs(t=64)
+        cache = compress(k, v, ResKVKernelConfig(bits=bits, sparsity=0.75, layout=layout), clustering=c)
+        out = attention(q, cache, position=64)
+    stream.synchronize()
+    assert _max_err(out, expected_attention(q, cache, position=64)) <= ATOL
+
+
+@pytest.mark.parametrize("ratio", [1, 8])
+@pytest.mark.parametrize("bits,layout", [(16, "unstructured"), (16, "structured"), (4, "structured"),
+                                         (2, "unstructured")])
+def test_gqa_and_64_centroids(device, ratio, bits, layout):
+    k, v, q, _ = reference_test_inputs(t=320)
+    q = q[:, :1].repeat(1, ratio, 1, 1)
+    centers = k[:, :, :64].contiguous()
+    ids = torch.arange(320, device=device, dtype=torch.int32).remainder(64).view(1, 1, -1)
+    cfg = ResKVKernelConfig(bits=bits, sparsity=0.75, layout=layout)
+    cache = compress(k, v, cfg, clustering=((centers, ids), (centers, ids)))
+    out = attention(q, cache, position=330, start_position=10)
+    assert _max_err(out, expected_attention(q, cache, position=330, start_position=10)) <= ATOL
+
+
+def test_structured_int4_large_logits(device):
+    k, v, q, c = reference_test_inputs(t=256)
+    k, q = k * 12, q * 12
+    cfg = ResKVKernelConfig(bits=4, sparsity=0.75, layout="structured", centroid_fusion="deferred")
+    cache = compress(k, v, cfg, clustering=c)
+    out = attention(q, cache, position=256)
+    assert torch.isfinite(out).all()
+    assert _max_err(out, expected_attention(q, cache, position=256)) <= ATOL
+
+
+def test_invalid_external_cluster_ids_rejected(device):
+    k, v, _, c = reference_test_inputs(t=64)
+    c[0][1][0, 0, 0] = 32
+    with pytest.raises(ValueError, match="out of range"):
+        compress(k, v, clustering=c)
+
+
+def test_theta_rope_with_model_rotated_recent_tokens(device):
+    k, v, q, c = reference_test_inputs(t=256)
+    cfg = ResKVKernelConfig(bits=4, sparsity=0.75, layout="unstructured", rope_mode="theta")
+    cache = compress(k, v, cfg, clustering=c)
+    model_freq = theta_freq() / 8
+    qr = torch.from_numpy(o.rotate(np_(q).astype(np.float64), np.array([288]), np_(model_freq))).half().to(device)
+    recent = (qr, k[:, :, :32].contiguous(), v[:, :, :32].contiguous())
+    out = attention(q, cache, position=288, recent=recent)
+    assert _max_err(out, expected_attention(q, cache, position=288, recent=recent)) <= ATOL
+
+
+@pytest.mark.parametrize("sparsity", [0.5, 0.75])
+def test_recent_attention_with_large_finite_scores(device, sparsity):
+    data = torch.zeros(1, 1, 128, 128, device=device, dtype=torch.float16)
+    centers = data[:, :, :1].contiguous()
+    ids = torch.zeros(1, 1, 128, device=device, dtype=torch.int32)
+    config = ResKVKernelConfig(sparsity=sparsity, centroid_fusion="deferred")
+    cache = compress(data, data, config, clustering=((centers, ids), (centers, ids)))
+    query = torch.full((1, 4, 1, 128), 100.0, device=device, dtype=torch.float16)
+    recent = (query, torch.full_like(data[:, :, :32], 100.0), torch.full_like(data[:, :, :32], 2.0))
+    out = attention(query, cache, position=159, recent=recent)
+    assert torch.isfinite(out).all()
+    ref = expected_attention(query, cache, position=159, recent=recent)
+    assert np.allclose(np_(out).astype(np.float64), ref, atol=1e-3, rtol=1e-3)
+
+
+@pytest.mark.parametrize("sparsity,layout", [(0.5, "unstructured"), (0.75, "structured"),
+                                             (0.75, "unstructured")])
+def test_config0_outlier_keys(device, sparsity, layout):
+    """Config 0 shapes and distributions (B=1, 8/32 heads, T=1024, sinks 4, recent 60)."""
+    k, v, q = outlier_kv(1, 8, 1024, seed=0)
+    freq = theta_freq()
+    sink, tc = 4, 960
+    cfg = ResKVKernelConfig(sparsity=sparsity, layout=layout, num_clusters=32, kmeans_iterations=15)
+    cache = compress(k[:, :, sink:sink + tc].contiguous(), v[:, :, sink:sink + tc].contiguous(), cfg)
+    dense_pos = torch.cat((torch.arange(sink), torch.arange(sink + tc, 1024))).numpy()
+    k_dense = np_(k)[:, :, dense_pos].astype(np.float64)
+    kr = torch.from_numpy(o.rotate(k_dense, dense_pos, np_(freq))).half().to(device)
+    vr = v[:, :, dense_pos].contiguous()
+    qr = torch.from_numpy(o.rotate(np_(q).astype(np.float64), np.array([1024]), np_(freq))).half().to(device)
+    out = attention(q, cache, position=1024, start_position=sink, inv_freq=freq, recent=(qr, kr, vr))
+    ref = expected_attention(q, cache, position=1024, start_position=sink, inv_freq=freq, recent=(qr, kr, vr))
+    assert _max_err(out, ref) <= ATOL
+
+
+@pytest.mark.parametrize("layout,sparsity", [("unstructured", 0.5), ("structured", 0.75)])
+def test_split_count_invariance_and_stats(device, layout, sparsity):
+    from reskv_amd._extension import load_extension
+
+    k, v, q = outlier_kv(2, 2, 700, seed=9, gqa=4)
+    cfg = ResKVKernelConfig(sparsity=sparsity, layout=layout, centroid_fusion="deferred", num_clusters=16)
+    cache = compress(k, v, cfg)
+    ext = load_extension("cluster_mass", cache.key.plan)
+    qf = q.reshape(-1, 128).contiguous()
+    kc, ki, kp, km, _ = cache.key._native
+    vc, vi, vp, vm, _ = cache.value._native
+    freq = theta_freq()
+    args = (2, 8, 0, 800, 500000.0, 128 ** -0.5, True)
+    outs = []
+    for splits in (1, 3, 64, 700, 0):
+        if layout == "unstructured":
+            o_, m_, l_ = ext.decode_fp16(qf, kc, ki, kp, km, vc, vi, vp, vm, *args, splits, freq)
+        else:
+            e = qf.new_empty(0)
+            o_, m_, l_ = ext.decode_structured_fp16(qf, kc, ki, kp, km, e, vc, vi, vp, vm, e, *args, splits, freq)
+        outs.append((np_(o_).astype(np.float64), np_(m_), np_(l_)))
+    eo, em, el = o.compressed_stats(np_(q).astype(np.float64), _dense(cache.key), _dense(cache.value),
+                                    position=800, freq=np_(freq))
+    for o_, m_, l_ in outs:
+        assert np.abs(o_ - eo.reshape(-1, 128)).max() <= ATOL
+        assert np.allclose(m_, em.reshape(-1), atol=1e-3, rtol=1e-4)
+        assert np.allclose(l_, el.reshape(-1), rtol=2e-4)
+
+
+def _dense(ct):
+    from tests.gpu_helpers import dense
+
+    return dense(ct)
+
+
+def test_dense_baseline_decode(device):
+    from reskv_amd._extension import dense_decode
+
+    k, v, q = outlier_kv(2, 4, 513, seed=4, gqa=8)
+    freq = theta_freq()
+    out = dense_decode(q, k, v, freq, position=600, start_position=3)
+    ref = o.reference_attention(np_(q).astype(np.float64), np_(k).astype(np.float64), np_(v).astype(np.float64),
+                                position=600, start_position=3, freq=np_(freq))
+    assert _max_err(out, ref) <= ATOL
+
+
+def test_query_position_before_cache_rejected(device):
+    k, v, q, c = reference_test_inputs(t=64)
+    cache = compress(k, v, clustering=c)
+    with pytest.raises(ValueError, match="precedes"):
+        attention(q, cache, position=10)

@@ -1,0 +1,88 @@
+"""HIP k-means vs the float64 oracle.
+
+Assignments must be equal wherever the oracle's nearest/second-nearest margin
+exceeds fp32 rounding; centres agree within fp16 rounding of the member mean.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import reskv_oracle as o
+from reskv_amd.compression import _incremental_cluster, cluster
+from reskv_amd import ResKVKernelConfig
+from tests.gpu_helpers import np_, outlier_kv, seeded
+
+pytestmark = pytest.mark.gpu
+
+
+def _tie_free_equal(gpu_ids, ora_ids, margin, data):
+    scale = float(np.abs(data).max()) ** 2 * 128
+    safe = margin > 1e-5 * scale
+    assert safe.mean() > 0.98
+    assert np.array_equal(gpu_ids[safe], ora_ids[safe])
+
+
+@pytest.mark.parametrize("value", [False, True])
+def test_single_iteration_matches_oracle(device, value):
+    x, _, _ = outlier_kv(1, 4, 1000, seed=21) if not value else (None, None, None)
+    if value:
+        _, x, _ = outlier_kv(1, 4, 1000, seed=22)
+    centers, ids = cluster(x, 32, 1, value=value)
+    ec, eids, _ = o.kmeans(np_(x), 32, 1, value=value)
+    data = np_(x).astype(np.float64).reshape(4, 1000, 128)
+    init = data[:, o.linspace_indices(1000, 32)]
+    _, margin = o.assign(data, init)
+    _tie_free_equal(np_(ids).reshape(4, -1), eids.reshape(4, -1), margin, data)
+    if np.array_equal(np_(ids), eids):
+        ref = ec.astype(np.float64)
+        got = np_(centers).astype(np.float64)
+        assert np.abs(got - ref).max() <= 2e-3 * max(1.0, np.abs(ref).max())
+
+
+@pytest.mark.parametrize("value", [False, True])
+def test_separated_mixture_full_run(device, value):
+    g = seeded(3)
+    means = torch.randn(1, 2, 8, 128, generator=g) * 4
+    member = torch.randint(8, (1, 2, 2048), generator=g)
+    x = means.gather(2, member[..., None].expand(-1, -1, -1, 128)) + torch.randn(1, 2, 2048, 128, generator=g) * 0.3
+    x = x.half().to(device)
+    centers, ids = cluster(x, 8, 10, value=value)
+    ec, eids, margin = o.kmeans(np_(x), 8, 10, value=value)
+    assert np.array_equal(np_(ids), eids)
+    assert np.abs(np_(centers).astype(np.float64) - ec.astype(np.float64)).max() <= 4e-3
+
+
+@pytest.mark.parametrize("count", [1, 32])
+def test_value_cluster_mean_does_not_overflow(device, count):
+    # known answer of reskv tests/test_cuda.py:161-169
+    data = torch.full((1, 1, 8192, 128), 20.0, device=device, dtype=torch.float16)
+    centers, assignments = cluster(data, count=count, iterations=2, value=True)
+    assert torch.isfinite(centers).all()
+    restored = centers.gather(2, assignments.long().unsqueeze(-1).expand_as(data))
+    assert torch.equal(restored, data)
+
+
+def test_short_input_key_clustering(device):
+    x = torch.randn(1, 2, 5, 128, device=device).half()
+    centers, ids = cluster(x, 8, 3)
+    assert centers.shape == (1, 2, 8, 128) and torch.isfinite(centers).all()
+    assert int(ids.min()) >= 0 and int(ids.max()) < 8
+    vc, vi = cluster(x, 8, 3, value=True)  # V caps the count at T
+    assert vc.shape == (1, 2, 5, 128)
+
+
+def test_incremental_cluster_matches_oracle(device):
+    g = seeded(8)
+    x = torch.randn(2, 2, 64, 128, generator=g).half().to(device)
+    c = torch.randn(2, 2, 20, 128, generator=g).half().to(device)
+    cfg = ResKVKernelConfig(max_clusters=21)
+    c2, ids = _incremental_cluster(x, c, cfg)
+    ec, eids, _ = o.incremental_cluster(np_(x), np_(c), 21)
+    assert c2.shape[2] == 21
+    assert np.abs(np_(c2).astype(np.float64) - ec.astype(np.float64)).max() <= 1e-3
+    data = np_(x).astype(np.float64).reshape(4, 64, 128)
+    _, margin = o.assign(data, np_(c2).astype(np.float64).reshape(4, 21, 128))
+    _tie_free_equal(np_(ids).reshape(4, -1), eids.reshape(4, -1), margin, data)
+    c3, _ = _incremental_cluster(x, c2, cfg)  # at the cap: no new centre
+    assert c3.shape[2] == 21
