@@ -6,15 +6,15 @@ synthetic KV following reskv benchmarks/kernels.py:57-65 (k, v ~ 0.5 N(0,1),
 centroids ~ 0.1 N(0,1), random cluster ids, seed 42).  One *step* is one
 decode step of a 32-layer model: 32 fused decode-attention calls, each on its
 own layer cache (32 distinct caches, so the 256 MB Infinity Cache cannot hold
-the working set).  ``value`` = batch * steps / elapsed (tokens/s).
+the working set).  The step is captured once in a HIP graph and replayed, so
+the timed region holds only GPU work (the eager, Python-dispatched time per
+call is reported next to it).  ``value`` = batch * steps / elapsed (tokens/s).
 
-The JSON line also carries the roofline of the decode attention (algorithmic
-compressed bytes per call / measured time per call vs 8 TB/s) and a CPU
-baseline: the numpy oracle (reconstruct + float64 attention) on a bounded
-sample, timed on this host.
-
-``--sweep`` additionally measures every batch size and sparsity of config 2
-plus the dense fp16 baseline and prints one JSON line per point.
+The JSON line also carries the roofline of one decode-attention call
+(algorithmic compressed bytes per call / measured time per call vs 8 TB/s),
+a sweep over the batch sizes and sparsities of config 2 plus the dense fp16
+baseline at the same shapes, and a CPU baseline: the numpy oracle
+(reconstruct + float64 attention) on a bounded sample, timed on this host.
 """
 
 import argparse
@@ -27,6 +27,7 @@ HBM_PEAK = 8.0e12  # bytes/s, MI355X HBM3E
 METRIC = "decode tok/s, Llama-3.1-8B-shape 8K ctx bs1-32; attn µs/step + % HBM peak"
 LAYERS = 32
 HQ, HK, D, T = 32, 8, 128, 8192
+BATCHES = (1, 4, 8, 16, 32)
 
 
 def parse():
@@ -39,22 +40,27 @@ def parse():
     p.add_argument("--layout", default="auto")
     p.add_argument("--seq-len", type=int, default=T)
     p.add_argument("--layers", type=int, default=LAYERS)
-    p.add_argument("--sweep", action="store_true")
+    p.add_argument("--splits", type=int, default=0, help="split-K count (0: automatic)")
+    p.add_argument("--no-sweep", action="store_true")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
+    p.add_argument("--calibrate-copy", action="store_true",
+                   help="also run a 256 MiB device copy (reference point for HBM byte counters)")
     return p.parse_args()
 
 
 def algorithmic_bytes(plan, b, t, nc_k, nc_v):
-    """Compressed bytes one decode call must read (+ q read, out write)."""
+    """Compressed bytes one decode call must read (+ q read, out write).
+
+    Per (batch, kv-head): T * (2 int8 ids + K/V payload + K/V metadata + K/V
+    scales) + both centroid tables; per query head: q in, out written (fp16).
+    """
     if plan is None:  # dense fp16
         per_tok = 2 * D * 2
         cent = 0
     else:
         if plan.bits == 16:
-            payload = 2 * plan.nnz
-            meta = 16
-            scale = 0
+            payload, meta, scale = 2 * plan.nnz, 16, 0
         elif plan.layout == "structured":
             payload, meta, scale = 16, 8, 2
         else:
@@ -66,19 +72,19 @@ def algorithmic_bytes(plan, b, t, nc_k, nc_v):
 
 def build_caches(torch, b, t, sparsity, layout, layers, device):
     from reskv_amd import ResKVKernelConfig, compress
+    from reskv_amd.tensors import CompressedKV, CompressedTensor
 
     cfg = ResKVKernelConfig(sparsity=sparsity, layout=layout)
-    torch.manual_seed(42)
+    g = torch.Generator(device=device).manual_seed(42)
     shape = (b, HK, t, D)
-    k = torch.randn(shape, device=device, dtype=torch.float16) * 0.5
-    v = torch.randn_like(k) * 0.5
-    kc = torch.randn(b, HK, 32, D, device=device, dtype=torch.float16) * 0.1
-    vc = torch.randn_like(kc) * 0.1
-    ki = torch.randint(32, (b, HK, t), device=device, dtype=torch.int32)
-    vi = torch.randint(32, (b, HK, t), device=device, dtype=torch.int32)
+    k = torch.randn(shape, device=device, dtype=torch.float16, generator=g) * 0.5
+    v = torch.randn(shape, device=device, dtype=torch.float16, generator=g) * 0.5
+    kc = torch.randn(b, HK, 32, D, device=device, dtype=torch.float16, generator=g) * 0.1
+    vc = torch.randn(b, HK, 32, D, device=device, dtype=torch.float16, generator=g) * 0.1
+    ki = torch.randint(32, (b, HK, t), device=device, dtype=torch.int32, generator=g)
+    vi = torch.randint(32, (b, HK, t), device=device, dtype=torch.int32, generator=g)
     base = compress(k, v, cfg, clustering=((kc, ki), (vc, vi)))
     del k, v
-    from reskv_amd.tensors import CompressedKV, CompressedTensor
 
     def clone(ct):
         return CompressedTensor(ct.centroids.clone(), ct.cluster_ids.clone(), ct.payload.clone(),
@@ -86,72 +92,98 @@ def build_caches(torch, b, t, sparsity, layout, layers, device):
                                 None if ct.scale is None else ct.scale.clone(), ct.plan)
 
     caches = [base] + [CompressedKV(clone(base.key), clone(base.value)) for _ in range(layers - 1)]
-    q = torch.randn(b, HQ, 1, D, device=device, dtype=torch.float16)
+    q = torch.randn(b, HQ, 1, D, device=device, dtype=torch.float16, generator=g)
     return caches, q
 
 
-def time_steps(torch, fn, steps, warmup):
-    for _ in range(warmup):
+def graph_time(torch, fn, steps, warmup):
+    """Seconds for `steps` replays of a graph holding one call of fn()."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()  # eager warm-up outside the capture (library load, allocator)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
         fn()
+    for _ in range(warmup):
+        graph.replay()
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
     for _ in range(steps):
-        fn()
+        graph.replay()
     end.record()
     end.synchronize()
-    return start.elapsed_time(end) / 1e3  # seconds
+    del graph
+    return start.elapsed_time(end) / 1e3
 
 
-def measure_point(torch, b, t, sparsity, layout, layers, steps, warmup, device):
+def eager_time(torch, fn, steps):
+    fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    return time.perf_counter() - t0
+
+
+def measure_point(torch, b, t, sparsity, layout, layers, steps, warmup, splits, device, eager=False):
     from reskv_amd import attention
 
     caches, q = build_caches(torch, b, t, sparsity, layout, layers, device)
     freq = (500000.0 ** (-torch.arange(64, device=device).float() / 64)).float()
-    pos = t
 
     def step():
         for c in caches:
-            attention(q, c, position=pos, inv_freq=freq)
+            attention(q, c, position=t, inv_freq=freq, splits=splits)
 
-    secs = time_steps(torch, step, steps, warmup)
+    secs = graph_time(torch, step, steps, warmup)
+    per_call = secs / (steps * layers)
+    out = {}
+    if eager:
+        out["eager_us_per_layer_step"] = eager_time(torch, step, max(2, steps // 4)) / (max(2, steps // 4) * layers) * 1e6
     plan = caches[0].key.plan
     nbytes = algorithmic_bytes(plan, b, t, caches[0].key.centroids.shape[2], caches[0].value.centroids.shape[2])
-    per_call = secs / (steps * layers)
+    from reskv_amd import _lib
+
+    nsplit = _lib.lib().reskv_decode_splits(b, HQ, HK, t, splits)
     del caches
     torch.cuda.empty_cache()
-    return {
+    out.update({
         "batch": b, "sparsity": sparsity, "layout": plan.layout, "fusion": plan.centroid_fusion,
-        "seconds": secs, "us_per_layer_step": per_call * 1e6, "bytes_per_call": nbytes,
+        "splits": nsplit, "seconds": secs, "us_per_layer_step": per_call * 1e6, "bytes_per_call": nbytes,
         "achieved_GBps": nbytes / per_call / 1e9, "frac": nbytes / per_call / HBM_PEAK,
         "tokens_per_s": b * steps / secs,
-    }
+    })
+    return out
 
 
 def measure_dense(torch, b, t, layers, steps, warmup, device):
     from reskv_amd._extension import dense_decode
 
-    torch.manual_seed(43)
-    ks = [torch.randn(b, HK, t, D, device=device, dtype=torch.float16) * 0.5 for _ in range(min(layers, 4))]
-    vs = [torch.randn_like(ks[0]) * 0.5 for _ in range(len(ks))]
-    q = torch.randn(b, HQ, 1, D, device=device, dtype=torch.float16)
+    g = torch.Generator(device=device).manual_seed(43)
+    n = max(2, min(layers, (2 << 30) // (b * HK * t * D * 2 * 2)))  # distinct caches, >= 2 GB total
+    ks = [torch.randn(b, HK, t, D, device=device, dtype=torch.float16, generator=g) * 0.5 for _ in range(n)]
+    vs = [torch.randn(b, HK, t, D, device=device, dtype=torch.float16, generator=g) * 0.5 for _ in range(n)]
+    q = torch.randn(b, HQ, 1, D, device=device, dtype=torch.float16, generator=g)
     freq = (500000.0 ** (-torch.arange(64, device=device).float() / 64)).float()
-    n = len(ks)
 
     def step():
         for i in range(layers):
             dense_decode(q, ks[i % n], vs[i % n], freq, position=t)
 
-    secs = time_steps(torch, step, steps, warmup)
+    secs = graph_time(torch, step, steps, warmup)
     per_call = secs / (steps * layers)
     nbytes = algorithmic_bytes(None, b, t, 0, 0)
     del ks, vs
     torch.cuda.empty_cache()
     return {"batch": b, "us_per_layer_step": per_call * 1e6, "achieved_GBps": nbytes / per_call / 1e9,
-            "frac": nbytes / per_call / HBM_PEAK, "caches": n}
+            "frac": nbytes / per_call / HBM_PEAK, "distinct_caches": n}
 
 
-def cpu_baseline(seconds_budget, b, t, sparsity):
+def cpu_baseline(seconds_budget, t, sparsity):
     """numpy oracle decode (reconstruct + float64 attention) on one batch element."""
     import numpy as np
 
@@ -182,20 +214,40 @@ def cpu_baseline(seconds_budget, b, t, sparsity):
         one()
         n += 1
     per_elem = (time.perf_counter() - t0) / n
-    cores = len(os.sched_getaffinity(0))
-    # a decode step of the workload = LAYERS calls x b batch elements
-    return {"value": 1.0 / (LAYERS * per_elem), "unit": "tokens/s", "cores": cores, "kind": "port",
-            "sample": f"numpy oracle: reconstruct + float64 attention, 1 batch element x {HK} KV heads x "
-                      f"T={t}, bitmap {int(sparsity * 100)}% sparsity, {n} repetitions "
+    return {"value": 1.0 / (LAYERS * per_elem), "unit": "tokens/s", "cores": 1, "kind": "port",
+            "sample": f"numpy oracle (single-threaded BLAS-free float64 path): reconstruct + attention for 1 batch "
+                      f"element x {HK} KV heads x T={t}, bitmap {int(sparsity * 100)}% sparsity, {n} repetitions "
                       f"({per_elem * 1e3:.1f} ms each); tokens/s = 1 / ({LAYERS} layers x time per element)"}
+
+
+def measured_traffic(b, t, sparsity, layout):
+    """HBM bytes per launch of the partial kernel from the committed rocprof run, if it is this workload.
+
+    The figure comes from two rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE),
+    each scaled by what the same counter reads for a device copy of known
+    size; profiles/decode_partial_b32_s50.md holds the runs and the commands.
+    """
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "decode_traffic.json")
+    try:
+        with open(path) as f:
+            rec = json.load(f)
+    except (OSError, ValueError):
+        return None
+    w = rec.get("workload", {})
+    if (w.get("batch"), w.get("seq_len"), w.get("sparsity"), w.get("layout")) != (b, t, sparsity, layout):
+        return None
+    return (rec["fetch_bytes"] + rec["write_bytes"]) * 1000
 
 
 def main():
     args = parse()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU only; multi-GPU sharding is design-only "
-                                   "(see DESIGN.md)", "n_gpus": args.gpus}))
+        print(json.dumps({"error": "this build runs on one GPU; multi-GPU sharding is a design note only "
+                                   "(DESIGN.md), so --gpus above 1 is not supported", "n_gpus": args.gpus}))
         sys.exit(2)
+    # keep numpy's CPU baseline single-threaded so `cores` is what was used
+    for var in ("OMP_NUM_THREADS", "OPENBLAS_NUM_THREADS", "MKL_NUM_THREADS"):
+        os.environ[var] = "1"
     import torch
 
     if not torch.cuda.is_available():
@@ -203,19 +255,34 @@ def main():
         sys.exit(1)
     device = "cuda:0"
     torch.cuda.set_device(0)
-    if args.sweep:
-        for sparsity in (0.5, 0.75):
-            for b in (1, 4, 8, 16, 32):
-                r = measure_point(torch, b, args.seq_len, sparsity, args.layout, args.layers, args.steps,
-                                  args.warmup, device)
-                print(json.dumps({"sweep": r}), flush=True)
-        for b in (1, 4, 8, 16, 32):
-            print(json.dumps({"dense": measure_dense(torch, b, args.seq_len, args.layers, args.steps,
-                                                     args.warmup, device)}), flush=True)
+    if args.calibrate_copy:
+        src = torch.empty(256 << 20, dtype=torch.uint8, device=device).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     r = measure_point(torch, args.batch, args.seq_len, args.sparsity, args.layout, args.layers, args.steps,
-                      args.warmup, device)
-    dense = measure_dense(torch, args.batch, args.seq_len, args.layers, max(2, args.steps // 4), 1, device)
-    cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds, args.batch, args.seq_len, args.sparsity)
+                      args.warmup, args.splits, device, eager=True)
+    print(json.dumps({"point": r}), flush=True)
+    sweep, dense = [], []
+    if not args.no_sweep:
+        for sparsity in (0.5, 0.75):
+            for b in BATCHES:
+                s = measure_point(torch, b, args.seq_len, sparsity, args.layout, args.layers,
+                                  max(5, args.steps // 2), 2, args.splits, device)
+                sweep.append({k: s[k] for k in ("batch", "sparsity", "layout", "splits", "us_per_layer_step",
+                                                "achieved_GBps", "frac")})
+                print(json.dumps({"sweep": s}), flush=True)
+        for b in BATCHES:
+            d = measure_dense(torch, b, args.seq_len, args.layers, max(5, args.steps // 2), 2, device)
+            dense.append(d)
+            print(json.dumps({"dense": d}), flush=True)
+    dense_b = next((d for d in dense if d["batch"] == args.batch), None)
+    if dense_b is None:
+        dense_b = measure_dense(torch, args.batch, args.seq_len, args.layers, max(5, args.steps // 2), 2, device)
+    cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds, args.seq_len, args.sparsity)
+    traffic = measured_traffic(args.batch, args.seq_len, args.sparsity, r["layout"])
     secs = r["seconds"]
     line = {
         "metric": METRIC,
@@ -231,18 +298,23 @@ def main():
         "dtype": "fp32",
         "data": "synthetic",
         "config": {
-            "workload": f"config2 compressed-KV decode attention, {args.layers} layers x 1 decode step",
+            "workload": f"config 2 compressed-KV decode attention, one decode step = {args.layers} layer calls "
+                        f"(graph-replayed), batch {args.batch}, T={args.seq_len}, sparsity {args.sparsity}",
             "batch": args.batch, "seq_len": args.seq_len, "q_heads": HQ, "kv_heads": HK, "head_dim": D,
             "sparsity": args.sparsity, "layout": r["layout"], "centroid_fusion": r["fusion"],
-            "storage": "fp16 residuals, int8 ids", "attn_us_per_layer_step": r["us_per_layer_step"],
-            "dense_fp16_us_per_layer_step": dense["us_per_layer_step"],
-            "speedup_vs_dense": dense["us_per_layer_step"] / r["us_per_layer_step"],
+            "splits": r["splits"], "storage": "fp16 residuals + int8 ids, fp32 arithmetic",
+            "attn_us_per_layer_step": r["us_per_layer_step"],
+            "eager_us_per_layer_step": r["eager_us_per_layer_step"],
+            "dense_fp16_us_per_layer_step": dense_b["us_per_layer_step"],
+            "speedup_vs_dense": dense_b["us_per_layer_step"] / r["us_per_layer_step"],
             "parallelism": "single GPU",
+            "sweep": sweep,
+            "dense_sweep": [{k: d[k] for k in ("batch", "us_per_layer_step", "frac")} for d in dense],
         },
         "roofline": {
             "bound": "hbm", "achieved": r["achieved_GBps"], "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-            "frac": r["frac"], "traffic": None,
-            "kernel": "decode_partial_kernel + decode_merge_kernel (one attention call)",
+            "frac": r["frac"], "traffic": traffic,
+            "kernel": "one decode-attention call (decode_partial_kernel + decode_merge_kernel)",
             "bytes_per_call": r["bytes_per_call"],
         },
         "cpu_baseline": cpu,

@@ -374,7 +374,8 @@ def kmeans(x, count, iterations, *, value=False):
     """Lloyd k-means per (batch, head), float64 (compression.py:19-53).
 
     x: fp16 [B, H, T, 128].  K (value=False) keeps an empty cluster's previous
-    centre; V (value=True) zeroes it and uses count = min(count, T).
+    centre; V (value=True) zeroes it, rounds every updated centre to fp16 and
+    uses count = min(count, T).
     Returns (centers fp16 [B,H,C,128], ids int32 [B,H,T], min_margin float) where
     ids come from the last assignment (made against the pre-update centres)
     and centres from the last update.  Requires T >= count (the reference's
@@ -397,7 +398,8 @@ def kmeans(x, count, iterations, *, value=False):
         counts = onehot.sum(1)[..., None]
         sums = np.swapaxes(onehot, 1, 2) @ data
         mean = sums / np.maximum(counts, 1)
-        centers = mean if value else np.where(counts > 0, mean, centers)
+        # V centres are stored back in fp16 after every update (compression.py:48-50)
+        centers = f16(mean).astype(np.float64) if value else np.where(counts > 0, mean, centers)
     return f16(centers.reshape(b, h, count, D)), ids.reshape(b, h, t).astype(np.int32), min_margin
 
 

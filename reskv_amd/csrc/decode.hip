@@ -1,4 +1,4 @@
-// Split-K fused decode attention over the compressed K/V cache.
+// Split-K fused decode attention over the compressed K/V cache (gfx950, wave64).
 //
 // Semantics (reskv/reference.py:59-91, reskv/csrc/cluster_mass.cu:4-11):
 //   k_t = c_k[id_k(t)] + r_k(t)            (pre-RoPE key, fp32)
@@ -7,14 +7,19 @@
 // The Value centroids are applied once after the split reduction:
 //   sum_t p_t c_v[id_v(t)] = sum_c beta_c c_v[c],  beta_c = sum_{t: id_v(t)=c} p_t.
 // RoPE angles are fl32(position * inv_freq[i]) for rotate-half pairs (i, i+64),
-// exactly as the reference oracle forms them.
+// exactly as the reference oracle forms them; each angle is reduced modulo 2*pi
+// with a three-part constant and evaluated by the hardware sin/cos.
 //
-// Kernel 1 (partial): one workgroup per (split, kv-head, batch).  Each wave owns
-// channels {lane, lane+64} and walks tokens of its split; it keeps an online
-// softmax state per query head of the GQA group: running max m, normaliser l,
-// unnormalised Value-residual sum delta[128] and cluster mass beta[nc].
-// Kernel 2 (merge): one wave per (batch, query head) rescales the split partials
-// to a common maximum, folds sum_c beta_c c_v[c] and normalises.
+// Partial kernel: one workgroup of 4 waves per (split, kv-head, batch).  A wave
+// walks 16-token tiles of its split.  Each tile's raw bytes (ids, metadata,
+// payload, scales) are copied with 16-byte loads into the wave's LDS stage,
+// prefetching the next tile into registers meanwhile.  Inside a tile the wave
+// works on four tokens at a time: lane L = 16 * row + i takes token 4 * step +
+// row and channels {4i..4i+3} u {64+4i..64+4i+3} (four RoPE pairs), so a score
+// is a 16-lane DPP row sum.  The online softmax runs per tile in the log2
+// domain; the cluster mass beta accumulates with LDS atomics.
+// Merge kernel: one wave per (batch, query head) rescales the split partials to
+// a common maximum, folds sum_c beta_c c_v[c] and normalises.
 #include "common.h"
 #include "../../include/reskv_hip.h"
 
@@ -24,259 +29,575 @@ using namespace reskv;
 
 namespace {
 
-constexpr int kFmtDense = 5;  // internal: uncompressed fp16 rows, no centroids
-constexpr int kWaves = 4;
-constexpr int kMaxSplits = 256;
+// residual formats as the kernels see them (the two quantised widths split)
+enum DFmt { D_BITMAP = 0, D_TILED, D_STRUCT16, D_SINT4, D_Q4, D_Q2, D_DENSE };
 
-struct CTensor {
-    const uint16_t* cent;
-    const int8_t* ids;
-    const void* payload;
-    const void* meta;
-    const uint16_t* scale;
-    int nc, fmt, width, bits;
+constexpr int kWaves = 4;
+constexpr int kThreads = kWaves * kWave;
+constexpr int kTile = 16;      // tokens per wave tile
+constexpr int kRows = 4;       // tokens processed together (one per 16-lane row)
+constexpr int kSteps = kTile / kRows;
+constexpr int kMaxSplits = 1024;
+constexpr int kPartStride = kDim + kMaxClusters + 2;  // cross-wave merge record
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+template <int F> struct Traits;
+template <> struct Traits<D_BITMAP> { static constexpr int MB = 16, PQ = 4; static constexpr bool SC = false, CENT = true; };
+template <> struct Traits<D_TILED> { static constexpr int MB = 16, PQ = 4; static constexpr bool SC = false, CENT = true; };
+template <> struct Traits<D_STRUCT16> { static constexpr int MB = 16, PQ = 1; static constexpr bool SC = false, CENT = true; };
+template <> struct Traits<D_SINT4> { static constexpr int MB = 8, PQ = 1; static constexpr bool SC = true, CENT = true; };
+template <> struct Traits<D_Q4> { static constexpr int MB = 0, PQ = 1; static constexpr bool SC = true, CENT = true; };
+template <> struct Traits<D_Q2> { static constexpr int MB = 0, PQ = 1; static constexpr bool SC = true, CENT = true; };
+template <> struct Traits<D_DENSE> { static constexpr int MB = 0, PQ = 4; static constexpr bool SC = false, CENT = false; };
+
+struct DTensor {
+    const uint16_t* cent;     // fp16 [BH, nc, 128] (null for dense)
+    const int8_t* ids;        // [BH, T] (null for dense)
+    const uint8_t* payload;   // [BH, T, pb bytes]
+    const uint8_t* meta;      // [BH, T, MB bytes] or null
+    const uint16_t* scale;    // fp16 [BH, T] or null
+    int nc, width, pb;        // pb: payload bytes per token, a multiple of 16
 };
 
-__device__ __forceinline__ uint64_t bitrev64(uint64_t v) {
-    return ((uint64_t)__builtin_bitreverse32((uint32_t)v) << 32) | __builtin_bitreverse32((uint32_t)(v >> 32));
+struct DParams {
+    const uint16_t* q;
+    DTensor k, v;
+    const float* inv_freq;
+    int Hq, H, T, start_pos, pos_q, splits;
+    float qscale;  // scaling * log2(e): scores come out in the log2 domain
+    int stage_k, stage_v;  // LDS stage bytes per wave for K and V
+    int region0;           // bytes of the centroid / merge region
+    float* pm;
+    float* pl;
+    float* pd;
+    float* pb;
+};
+
+// ---------------------------------------------------------------------------
+// RoPE sin/cos of an fp32 angle: n = rint(a / 2pi); r = a - n * 2pi with 2pi
+// split in three fp32 parts (exact products through FMA); the hardware sin/cos
+// then take r / 2pi in revolutions, |r / 2pi| <= 1/2.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void rope_sincos_fast(float angle, float& s, float& c) {
+    constexpr float kInv2Pi = 0.15915493667125702f;
+    const float n = __builtin_rintf(angle * kInv2Pi);
+    float r = __builtin_fmaf(-n, 6.2831854820251465f, angle);
+    r = __builtin_fmaf(-n, -1.7484555314695172e-07f, r);
+    r = __builtin_fmaf(-n, -6.8604980400235275e-15f, r);
+    const float x = r * kInv2Pi;
+    s = __builtin_amdgcn_sinf(x);
+    c = __builtin_amdgcn_cosf(x);
 }
 
-// Residual values of channels `lane` and `lane + 64` of compressed row `row`
-// (row = (b * H + h) * T + t, wave-uniform).  Format decoders follow
-// reskv/reference.py:12-47.
-__device__ __forceinline__ void decode_residual(const CTensor& ct, long row, int lane, float& r0, float& r1) {
-    r0 = 0.0f;
-    r1 = 0.0f;
-    switch (ct.fmt) {
-    case RESKV_FMT_BITMAP: {
-        // channel d <-> bit (63 - d % 64) of word d / 64; value index = rank
-        const uint64_t* mw = (const uint64_t*)ct.meta + row * 2;
-        const uint64_t w0 = mw[0], w1 = mw[1];
-        const uint64_t v0 = bitrev64(w0), v1 = bitrev64(w1);
-        const uint16_t* p = (const uint16_t*)ct.payload + row * ct.width;
-        const uint32_t k0 = lanes_below(v0);
-        const uint32_t k1 = (uint32_t)__builtin_popcountll(w0) + lanes_below(v1);
-        if (((v0 >> lane) & 1ull) && k0 < (uint32_t)ct.width) r0 = h2f(p[k0]);
-        if (((v1 >> lane) & 1ull) && k1 < (uint32_t)ct.width) r1 = h2f(p[k1]);
-        break;
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// ---------------------------------------------------------------------------
+// tile staging: global -> registers (prefetch) -> LDS
+// ---------------------------------------------------------------------------
+template <int F>
+struct Prefetch {
+    uint4 pay[Traits<F>::PQ];
+    uint4 meta;
+    int id;
+    float sc;
+};
+
+// Loads the raw bytes of tokens [row0, row0 + n) of one tensor (row0 = bh*T + t).
+template <int F>
+__device__ __forceinline__ void prefetch(const DTensor& X, long row0, int n, int lane, Prefetch<F>& P) {
+    using Tr = Traits<F>;
+    const int per_tok = X.pb >> 4;
+    const int pieces = n * per_tok;
+    const uint4* src = reinterpret_cast<const uint4*>(X.payload + row0 * X.pb);
+#pragma unroll
+    for (int i = 0; i < Tr::PQ; ++i) {
+        const int q = lane + kWave * i;
+        P.pay[i] = q < pieces ? src[q] : make_uint4(0, 0, 0, 0);
     }
-    case RESKV_FMT_TILED:
-    case RESKV_FMT_STRUCT16: {
-        // word w = code(tile 2w) | code(tile 2w+1) << 16
-        const uint32_t* mw = (const uint32_t*)ct.meta + row * 4;
-        const uint16_t* p = (const uint16_t*)ct.payload + row * ct.width;
-        const int per_tile = ct.width >> 3;
-        const int bit = lane & 15;
+    P.meta = make_uint4(0, 0, 0, 0);
+    if constexpr (Tr::MB == 16) {
+        if (lane < n) P.meta = reinterpret_cast<const uint4*>(X.meta + row0 * 16)[lane];
+    } else if constexpr (Tr::MB == 8) {
+        if (lane < n) {
+            const uint2 m = reinterpret_cast<const uint2*>(X.meta + row0 * 8)[lane];
+            P.meta.x = m.x;
+            P.meta.y = m.y;
+        }
+    }
+    P.id = 0;
+    if constexpr (Tr::CENT) {
+        if (lane < n) P.id = X.ids[row0 + lane];
+    }
+    P.sc = 0.0f;
+    if constexpr (Tr::SC) {
+        if (lane < n) P.sc = h2f(X.scale[row0 + lane]);
+    }
+}
+
+// Stage layout (bytes): payload [16][pb] | meta [16][MB] | ids int32[16] | scale f32[16]
+template <int F>
+__device__ __forceinline__ void stage_store(const Prefetch<F>& P, uint8_t* st, int pb, int lane) {
+    using Tr = Traits<F>;
+    const int pieces = kTile * (pb >> 4);
+    uint4* pay = reinterpret_cast<uint4*>(st);
+#pragma unroll
+    for (int i = 0; i < Tr::PQ; ++i) {
+        const int q = lane + kWave * i;
+        if (q < pieces) pay[q] = P.pay[i];
+    }
+    uint8_t* meta = st + kTile * pb;
+    if (lane < kTile) {
+        if constexpr (Tr::MB == 16) reinterpret_cast<uint4*>(meta)[lane] = P.meta;
+        if constexpr (Tr::MB == 8) reinterpret_cast<uint2*>(meta)[lane] = make_uint2(P.meta.x, P.meta.y);
+        int* ids = reinterpret_cast<int*>(meta + kTile * Tr::MB);
+        ids[lane] = P.id;
+        reinterpret_cast<float*>(ids + kTile)[lane] = P.sc;
+    }
+}
+
+template <int F>
+__host__ __device__ constexpr int stage_bytes(int pb) {
+    return kTile * pb + kTile * Traits<F>::MB + 2 * kTile * 4;
+}
+
+// ---------------------------------------------------------------------------
+// residual decoders (LDS stage -> 8 fp32 values of this lane's channels)
+// r[0..3] = channels 4i..4i+3, r[4..7] = channels 64+4i..64+4i+3
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float lds_h(const uint16_t* p, int idx) { return h2f(p[idx]); }
+
+// 4 channels of a 16-bit LSB-first tile mask: nib bit j = channel j; values at base + rank
+__device__ __forceinline__ void expand4(uint32_t nib, int base, const uint16_t* p, float* r) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int idx = base + __builtin_popcount(nib & ((1u << j) - 1u));
+        r[j] = ((nib >> j) & 1u) ? lds_h(p, idx) : 0.0f;
+    }
+}
+
+template <int F>
+__device__ __forceinline__ void decode_res(const uint8_t* st, int tok, int pb, int width, int li, float* r) {
+    using Tr = Traits<F>;
+    const uint8_t* payb = st + tok * pb;
+    const uint16_t* p16 = reinterpret_cast<const uint16_t*>(payb);
+    const uint8_t* meta = st + kTile * pb + tok * Tr::MB;
+    if constexpr (F == D_BITMAP) {
+        // channel d <-> bit (63 - d % 64) of word d / 64; value index = rank (reference.py:22-26)
+        const uint4 m = *reinterpret_cast<const uint4*>(meta);
+        const uint64_t w0 = (uint64_t)m.x | ((uint64_t)m.y << 32);
+        const uint64_t w1 = (uint64_t)m.z | ((uint64_t)m.w << 32);
+        const int sh = 60 - 4 * li;
+        const uint32_t na = (uint32_t)(w0 >> sh) & 15u, nb = (uint32_t)(w1 >> sh) & 15u;
+        // bits above this lane's nibble: (w >> 1) >> (63 - 4i) keeps every shift below 64
+        const int hi = 63 - 4 * li;
+        const int ba = li ? __builtin_popcountll((w0 >> 1) >> hi) : 0;
+        const int bb = __builtin_popcountll(w0) + (li ? __builtin_popcountll((w1 >> 1) >> hi) : 0);
+        // MSB-first: channel 4i+j is nibble bit 3-j; earlier channels are the higher bits
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int ia = ba + __builtin_popcount(na >> (4 - j));
+            const int ib = bb + __builtin_popcount(nb >> (4 - j));
+            r[j] = ((na >> (3 - j)) & 1u) ? lds_h(p16, ia) : 0.0f;
+            r[4 + j] = ((nb >> (3 - j)) & 1u) ? lds_h(p16, ib) : 0.0f;
+        }
+    } else if constexpr (F == D_TILED || F == D_STRUCT16) {
+        // word w = code(tile 2w) | code(tile 2w+1) << 16 (reference.py:36-47)
+        const uint4 m = *reinterpret_cast<const uint4*>(meta);
+        const uint32_t mw[4] = {m.x, m.y, m.z, m.w};
+        const int per_tile = F == D_TILED ? (width >> 3) : 4;
+        const int sub = li & 3;
 #pragma unroll
         for (int half = 0; half < 2; ++half) {
-            const int tile = (lane >> 4) + 4 * half;
-            const uint32_t code = (mw[tile >> 1] >> (16 * (tile & 1))) & 0xFFFFu;
-            int idx = -1;
-            if (ct.fmt == RESKV_FMT_TILED) {
-                if ((code >> bit) & 1u) idx = tile * per_tile + __builtin_popcount(code & ((1u << bit) - 1u));
-            } else {
+            const int tile = (li >> 2) + 4 * half;
+            uint32_t code = (mw[tile >> 1] >> (16 * (tile & 1))) & 0xFFFFu;
+            if (F == D_STRUCT16) {
+                // four ascending in-tile channel indices -> 16-bit mask
+                uint32_t mask = 0;
 #pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    if ((int)((code >> (4 * r)) & 15u) == bit) idx = tile * 4 + r;
+                for (int k = 0; k < 4; ++k) mask |= 1u << ((code >> (4 * k)) & 15u);
+                code = mask;
             }
-            const float val = (idx >= 0 && idx < ct.width) ? h2f(p[idx]) : 0.0f;
-            if (half == 0) r0 = val; else r1 = val;
+            const uint32_t nib = (code >> (4 * sub)) & 15u;
+            const int base = tile * per_tile + __builtin_popcount(code & ((1u << (4 * sub)) - 1u));
+            expand4(nib, base, p16, r + 4 * half);
         }
-        break;
-    }
-    case RESKV_FMT_STRUCT_INT4: {
-        const uint32_t* qp = (const uint32_t*)ct.payload + row * 4;
-        const uint32_t* qm = (const uint32_t*)ct.meta + row * 2;
-        const float s = h2f(ct.scale[row]);
+    } else if constexpr (F == D_SINT4) {
+        // 1 of 4 per subgroup: 2-bit position, signed nibble code, fp16 scale (reference.py:27-35)
+        const uint4 qp = *reinterpret_cast<const uint4*>(payb);
+        const uint2 qm = *reinterpret_cast<const uint2*>(meta);
+        const float s = reinterpret_cast<const float*>(st + kTile * pb + kTile * Tr::MB + kTile * 4)[tok];
+        const uint32_t qw[4] = {qp.x, qp.y, qp.z, qp.w};
 #pragma unroll
         for (int half = 0; half < 2; ++half) {
-            const int d = lane + 64 * half;
-            const int grp = d >> 2;
-            const int sel = (int)((qm[grp >> 4] >> (2 * (grp & 15))) & 3u);
-            float val = 0.0f;
-            if (sel == (d & 3)) {
-                const int nib = (int)((qp[grp >> 3] >> (4 * (grp & 7))) & 15u);
-                val = (float)((nib ^ 8) - 8) * s;
+            const int grp = li + 16 * half;
+            const uint32_t sel = ((half ? qm.y : qm.x) >> (2 * li)) & 3u;
+            const int code = (int)((qw[grp >> 3] >> (4 * (grp & 7))) & 15u);
+            const float val = (float)((code ^ 8) - 8) * s;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) r[4 * half + j] = (uint32_t)j == sel ? val : 0.0f;
+        }
+    } else if constexpr (F == D_Q4 || F == D_Q2) {
+        // signed codes, channel d in word d / (32/bits) at bit (d % (32/bits)) * bits (reference.py:17-21)
+        constexpr int bits = F == D_Q4 ? 4 : 2;
+        constexpr int per_word = 32 / bits;
+        constexpr int sign = 1 << (bits - 1);
+        const uint32_t* qw = reinterpret_cast<const uint32_t*>(payb);
+        const float s = reinterpret_cast<const float*>(st + kTile * pb + kTile * 4)[tok];
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+            const int d0 = 4 * li + 64 * half;
+            const uint32_t w = qw[d0 / per_word] >> ((d0 % per_word) * bits);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int code = (int)((w >> (j * bits)) & (uint32_t)((1 << bits) - 1));
+                r[4 * half + j] = (float)((code ^ sign) - sign) * s;
             }
-            if (half == 0) r0 = val; else r1 = val;
         }
-        break;
+    } else {  // dense fp16 rows
+        const uint2 a = *reinterpret_cast<const uint2*>(p16 + 4 * li);
+        const uint2 b = *reinterpret_cast<const uint2*>(p16 + 64 + 4 * li);
+        r[0] = h2f((uint16_t)(a.x & 0xFFFFu));
+        r[1] = h2f((uint16_t)(a.x >> 16));
+        r[2] = h2f((uint16_t)(a.y & 0xFFFFu));
+        r[3] = h2f((uint16_t)(a.y >> 16));
+        r[4] = h2f((uint16_t)(b.x & 0xFFFFu));
+        r[5] = h2f((uint16_t)(b.x >> 16));
+        r[6] = h2f((uint16_t)(b.y & 0xFFFFu));
+        r[7] = h2f((uint16_t)(b.y >> 16));
     }
-    case RESKV_FMT_QUANT: {
-        const uint32_t* qt = (const uint32_t*)ct.payload + row * ct.width;
-        const float s = h2f(ct.scale[row]);
-        const int bits = ct.bits, per_word = 32 / bits;
-        const int sign = 1 << (bits - 1), mask = (1 << bits) - 1;
-#pragma unroll
-        for (int half = 0; half < 2; ++half) {
-            const int d = lane + 64 * half;
-            const int code = (int)((qt[d / per_word] >> ((d % per_word) * bits)) & (uint32_t)mask);
-            const float val = (float)((code ^ sign) - sign) * s;
-            if (half == 0) r0 = val; else r1 = val;
-        }
-        break;
-    }
-    default: {  // dense fp16 rows
-        const uint16_t* p = (const uint16_t*)ct.payload + row * kDim;
-        r0 = h2f(p[lane]);
-        r1 = h2f(p[lane + 64]);
-        break;
-    }
-    }
+}
+
+template <int F>
+__device__ __forceinline__ int stage_id(const uint8_t* st, int pb, int tok) {
+    return reinterpret_cast<const int*>(st + kTile * pb + kTile * Traits<F>::MB)[tok];
 }
 
 __device__ __forceinline__ int clamp_id(int id, int nc) { return id < 0 ? 0 : (id >= nc ? nc - 1 : id); }
 
-template <int G>
-__global__ void __launch_bounds__(256) decode_partial_kernel(
-    const uint16_t* __restrict__ q, CTensor kt, CTensor vt, const float* __restrict__ inv_freq,
-    int Hq, int H, int T, int start_pos, int pos_q, float scaling, int splits,
-    float* __restrict__ pm, float* __restrict__ pl, float* __restrict__ pdelta, float* __restrict__ pbeta) {
+__device__ __forceinline__ float rows_max(float v) {
+    return fmaxf(fmaxf(readlane(v, 0), readlane(v, 16)), fmaxf(readlane(v, 32), readlane(v, 48)));
+}
+__device__ __forceinline__ float rows_sum(float v) {
+    return (readlane(v, 0) + readlane(v, 16)) + (readlane(v, 32) + readlane(v, 48));
+}
+// sum over the four rows, result in every lane (lanes i, i+16, i+32, i+48)
+__device__ __forceinline__ float cross_rows_sum(float v) {
+    v += __shfl_xor(v, 16);
+    v += __shfl_xor(v, 32);
+    return v;
+}
+
+// ---------------------------------------------------------------------------
+// partial kernel
+// ---------------------------------------------------------------------------
+template <int G, int KF, int VF>
+__global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    using KT = Traits<KF>;
+    using VT = Traits<VF>;
     const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-    const long bh = (long)b * H + h;
-    const int t0 = (int)(((long)split * T) / splits);
-    const int t1 = (int)(((long)(split + 1) * T) / splits);
+    const long bh = (long)b * P.H + h;
+    const int t0 = (int)(((long)split * P.T) / P.splits);
+    const int t1 = (int)(((long)(split + 1) * P.T) / P.splits);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int row = lane >> 4, li = lane & 15;
 
-    // K centroid table in fp32; reused afterwards for the cross-wave merge.
-    __shared__ float s_buf[kMaxClusters * kDim];
-    const bool dense = kt.fmt == kFmtDense;
-    if (!dense) {
-        const uint16_t* kc = kt.cent + bh * kt.nc * kDim;
-        for (int i = threadIdx.x; i < kt.nc * kDim; i += blockDim.x) s_buf[i] = h2f(kc[i]);
+    float* s_cent = reinterpret_cast<float*>(smem);                       // region 0
+    float* s_beta = reinterpret_cast<float*>(smem + P.region0);            // [wave][G][64]
+    const int beta_bytes = KT::CENT ? kWaves * G * kMaxClusters * 4 : 0;
+    uint8_t* st_k = smem + P.region0 + beta_bytes + wave * (P.stage_k + P.stage_v);
+    uint8_t* st_v = st_k + P.stage_k;
+    float* my_beta = s_beta + wave * G * kMaxClusters;
+
+    if constexpr (KT::CENT) {
+        const uint16_t* kc = P.k.cent + bh * P.k.nc * kDim;
+        for (int i = threadIdx.x; i < P.k.nc * kDim; i += kThreads) s_cent[i] = h2f(kc[i]);
+#pragma unroll
+        for (int g = 0; g < G; ++g) my_beta[g * kMaxClusters + lane] = 0.0f;
     }
-    __syncthreads();
 
-    const float freq = inv_freq[lane];
-    float qa[G], qb[G];
+    // rotated, pre-scaled query: qa = channels 4i+j, qb = channels 64+4i+j
+    const float4 fq = *reinterpret_cast<const float4*>(P.inv_freq + 4 * li);
+    const float freq[4] = {fq.x, fq.y, fq.z, fq.w};
+    float qa[G][4], qb[G][4];
     {
-        float s, c;
-        rope_sincos((float)pos_q, freq, &s, &c);
+        float sn[4], cs[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) rope_sincos_fast(__fmul_rn((float)P.pos_q, freq[j]), sn[j], cs[j]);
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-            const uint16_t* qr = q + ((long)b * Hq + (long)h * G + g) * kDim;
-            const float a = h2f(qr[lane]), bb = h2f(qr[lane + 64]);
-            qa[g] = a * c - bb * s;
-            qb[g] = bb * c + a * s;
+            const uint16_t* qr = P.q + ((long)b * P.Hq + (long)h * G + g) * kDim;
+            const uint2 ua = *reinterpret_cast<const uint2*>(qr + 4 * li);
+            const uint2 ub = *reinterpret_cast<const uint2*>(qr + 64 + 4 * li);
+            const float a[4] = {h2f(ua.x & 0xFFFFu), h2f(ua.x >> 16), h2f(ua.y & 0xFFFFu), h2f(ua.y >> 16)};
+            const float c[4] = {h2f(ub.x & 0xFFFFu), h2f(ub.x >> 16), h2f(ub.y & 0xFFFFu), h2f(ub.y >> 16)};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                qa[g][j] = (a[j] * cs[j] - c[j] * sn[j]) * P.qscale;
+                qb[g][j] = (c[j] * cs[j] + a[j] * sn[j]) * P.qscale;
+            }
         }
     }
 
-    float m[G], l[G], d0[G], d1[G], beta[G];
+    float m[G], l[G], dl[G][8];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
         m[g] = -INFINITY;
         l[g] = 0.0f;
-        d0[g] = d1[g] = beta[g] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) dl[g][j] = 0.0f;
     }
+    __syncthreads();
 
-    for (int t = t0 + wave; t < t1; t += kWaves) {
-        const long row = bh * T + t;
-        float kr0, kr1, vr0, vr1;
-        decode_residual(kt, row, lane, kr0, kr1);
-        decode_residual(vt, row, lane, vr0, vr1);
-        float k0 = kr0, k1 = kr1;
-        int vid = -1;
-        if (!dense) {
-            const int kid = clamp_id(kt.ids[row], kt.nc);
-            vid = clamp_id(vt.ids[row], vt.nc);
-            k0 += s_buf[kid * kDim + lane];
-            k1 += s_buf[kid * kDim + lane + 64];
+    const int ntiles = (t1 - t0 + kTile - 1) / kTile;
+    Prefetch<KF> pk;
+    Prefetch<VF> pv;
+    if (wave < ntiles) {
+        const int tb = t0 + wave * kTile;
+        const int n = min(kTile, t1 - tb);
+        prefetch<KF>(P.k, bh * P.T + tb, n, lane, pk);
+        prefetch<VF>(P.v, bh * P.T + tb, n, lane, pv);
+    }
+    for (int tile = wave; tile < ntiles; tile += kWaves) {
+        const int tb = t0 + tile * kTile;
+        const int n = min(kTile, t1 - tb);
+        stage_store<KF>(pk, st_k, P.k.pb, lane);
+        stage_store<VF>(pv, st_v, P.v.pb, lane);
+        wave_sync();
+        if (tile + kWaves < ntiles) {
+            const int tb2 = tb + kWaves * kTile;
+            const int n2 = min(kTile, t1 - tb2);
+            prefetch<KF>(P.k, bh * P.T + tb2, n2, lane, pk);
+            prefetch<VF>(P.v, bh * P.T + tb2, n2, lane, pv);
         }
-        float s, c;
-        rope_sincos((float)(start_pos + t), freq, &s, &c);
-        const float x0 = k0 * c - k1 * s;
-        const float x1 = k1 * c + k0 * s;
+
+        // ---- scores of the tile's 16 tokens (log2 domain) ----
+        float sc[G][kSteps];
+#pragma unroll
+        for (int s = 0; s < kSteps; ++s) {
+            const int tok = kRows * s + row;
+            float kr[8];
+            decode_res<KF>(st_k, tok, P.k.pb, P.k.width, li, kr);
+            if constexpr (KT::CENT) {
+                const int kid = clamp_id(stage_id<KF>(st_k, P.k.pb, tok), P.k.nc);
+                const float4 ca = *reinterpret_cast<const float4*>(s_cent + kid * kDim + 4 * li);
+                const float4 cb = *reinterpret_cast<const float4*>(s_cent + kid * kDim + 64 + 4 * li);
+                kr[0] += ca.x; kr[1] += ca.y; kr[2] += ca.z; kr[3] += ca.w;
+                kr[4] += cb.x; kr[5] += cb.y; kr[6] += cb.z; kr[7] += cb.w;
+            }
+            const float pos = (float)(P.start_pos + tb + tok);
+            float xa[4], xb[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                float sn, cs;
+                rope_sincos_fast(__fmul_rn(pos, freq[j]), sn, cs);
+                xa[j] = kr[j] * cs - kr[4 + j] * sn;
+                xb[j] = kr[4 + j] * cs + kr[j] * sn;
+            }
+            const bool valid = tok < n;
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                float part = 0.0f;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) part = fmaf(qa[g][j], xa[j], fmaf(qb[g][j], xb[j], part));
+                const float score = row_sum16(part);
+                sc[g][s] = valid ? score : -INFINITY;
+            }
+        }
+
+        // ---- online softmax over the tile ----
+        bool grow = false;
+        float mnew[G];
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-            const float score = wave_sum(qa[g] * x0 + qb[g] * x1) * scaling;
-            const float mn = fmaxf(m[g], score);
-            const float alpha = expf(m[g] - mn);
-            const float p = expf(score - mn);
-            l[g] = l[g] * alpha + p;
-            d0[g] = d0[g] * alpha + p * vr0;
-            d1[g] = d1[g] * alpha + p * vr1;
-            beta[g] = beta[g] * alpha + (lane == vid ? p : 0.0f);
-            m[g] = mn;
+            float mx = sc[g][0];
+#pragma unroll
+            for (int s = 1; s < kSteps; ++s) mx = fmaxf(mx, sc[g][s]);
+            mnew[g] = fmaxf(m[g], rows_max(mx));
+            grow |= mnew[g] > m[g];
         }
-    }
-    __syncthreads();  // centroid table no longer needed
+        if (grow) {
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                const float alpha = exp2_fast(m[g] - mnew[g]);  // 0 on the first tile
+                l[g] *= alpha;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) dl[g][j] *= alpha;
+                if constexpr (KT::CENT) my_beta[g * kMaxClusters + lane] *= alpha;
+                m[g] = mnew[g];
+            }
+            wave_sync();
+        }
+        float p[G][kSteps];
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+#pragma unroll
+            for (int s = 0; s < kSteps; ++s) {
+                p[g][s] = exp2_fast(sc[g][s] - m[g]);
+                l[g] += p[g][s];
+            }
+        }
 
-    // cross-wave merge through LDS: [wave][g][128 delta | 64 beta | m | l]
-    constexpr int kStride = kDim + kMaxClusters + 2;
-    float* mine = s_buf + (wave * G) * kStride;
+        // ---- values: residual sums and cluster mass ----
+#pragma unroll
+        for (int s = 0; s < kSteps; ++s) {
+            const int tok = kRows * s + row;
+            float vr[8];
+            decode_res<VF>(st_v, tok, P.v.pb, P.v.width, li, vr);
+#pragma unroll
+            for (int g = 0; g < G; ++g)
+#pragma unroll
+                for (int j = 0; j < 8; ++j) dl[g][j] = fmaf(p[g][s], vr[j], dl[g][j]);
+            if constexpr (VT::CENT) {
+                if (li < G) {
+                    float pg = p[0][s];
+#pragma unroll
+                    for (int g = 1; g < G; ++g) pg = li == g ? p[g][s] : pg;
+                    const int vid = clamp_id(stage_id<VF>(st_v, P.v.pb, tok), P.v.nc);
+                    atomicAdd(&my_beta[li * kMaxClusters + vid], pg);
+                }
+            }
+        }
+        wave_sync();  // stage reads done before the next tile overwrites it
+    }
+
+    // ---- fold the four rows, then merge the waves through LDS ----
+    float lt[G];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-        float* e = mine + g * kStride;
-        e[lane] = d0[g];
-        e[lane + 64] = d1[g];
-        e[kDim + lane] = beta[g];
+        lt[g] = rows_sum(l[g]);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) dl[g][j] = cross_rows_sum(dl[g][j]);
+    }
+    float bt[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) bt[g] = KT::CENT ? my_beta[g * kMaxClusters + lane] : 0.0f;
+    __syncthreads();  // centroid table and stages no longer needed
+    float* rec = reinterpret_cast<float*>(smem) + wave * G * kPartStride;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        float* e = rec + g * kPartStride;
+        if (row == 0) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                e[4 * li + j] = dl[g][j];
+                e[64 + 4 * li + j] = dl[g][4 + j];
+            }
+        }
+        e[kDim + lane] = bt[g];
         if (lane == 0) {
             e[kDim + kMaxClusters] = m[g];
-            e[kDim + kMaxClusters + 1] = l[g];
+            e[kDim + kMaxClusters + 1] = lt[g];
         }
     }
     __syncthreads();
     for (int g = wave; g < G; g += kWaves) {
+        const float* base = reinterpret_cast<const float*>(smem);
         float mx = -INFINITY;
-        for (int w = 0; w < kWaves; ++w) mx = fmaxf(mx, s_buf[(w * G + g) * kStride + kDim + kMaxClusters]);
-        float acc0 = 0.0f, acc1 = 0.0f, accb = 0.0f, accl = 0.0f;
         for (int w = 0; w < kWaves; ++w) {
-            const float* e = s_buf + (w * G + g) * kStride;
-            const float lw = e[kDim + kMaxClusters + 1];
-            const float sc = lw > 0.0f ? expf(e[kDim + kMaxClusters] - mx) : 0.0f;
-            acc0 += e[lane] * sc;
-            acc1 += e[lane + 64] * sc;
-            accb += e[kDim + lane] * sc;
-            accl += lw * sc;
+            const float* e = base + (w * G + g) * kPartStride;
+            if (e[kDim + kMaxClusters + 1] > 0.0f) mx = fmaxf(mx, e[kDim + kMaxClusters]);
         }
-        const long slot = ((long)b * Hq + (long)h * G + g) * splits + split;
-        pdelta[slot * kDim + lane] = acc0;
-        pdelta[slot * kDim + lane + 64] = acc1;
-        pbeta[slot * kMaxClusters + lane] = accb;
+        float a0 = 0.0f, a1 = 0.0f, ab = 0.0f, al = 0.0f;
+        for (int w = 0; w < kWaves; ++w) {
+            const float* e = base + (w * G + g) * kPartStride;
+            const float lw = e[kDim + kMaxClusters + 1];
+            const float f = lw > 0.0f ? exp2_fast(e[kDim + kMaxClusters] - mx) : 0.0f;
+            a0 += e[lane] * f;
+            a1 += e[lane + 64] * f;
+            ab += e[kDim + lane] * f;
+            al += lw * f;
+        }
+        const long slot = ((long)b * P.Hq + (long)h * G + g) * P.splits + split;
+        P.pd[slot * kDim + lane] = a0;
+        P.pd[slot * kDim + lane + 64] = a1;
+        P.pb[slot * kMaxClusters + lane] = ab;
         if (lane == 0) {
-            pm[slot] = mx;
-            pl[slot] = accl;
+            P.pm[slot] = mx;
+            P.pl[slot] = al;
         }
     }
 }
 
-// One wave per (batch, query head): combine the split partials.
-__global__ void __launch_bounds__(64) decode_merge_kernel(
+// One workgroup (256 threads) per (batch, query head) combines the split
+// partials (log2 domain).  Threads stride over the splits, so every global load
+// of the reduction is independent and many are in flight at once.
+constexpr int kMergeThreads = 256;
+
+__global__ void __launch_bounds__(kMergeThreads) decode_merge_kernel(
     const float* __restrict__ pm, const float* __restrict__ pl, const float* __restrict__ pdelta,
     const float* __restrict__ pbeta, const uint16_t* __restrict__ vcent, int vnc, int Hq, int H,
     int splits, uint16_t* __restrict__ out, float* __restrict__ om, float* __restrict__ ol) {
+    __shared__ float s_w[kMaxSplits];
+    __shared__ float s_red[kMergeThreads / kWave];
+    __shared__ float s_acc[2 * kDim + 4 * kMaxClusters];
     const long bq = blockIdx.x;  // b * Hq + hq
-    const int lane = threadIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int G = Hq / H;
     const long bh = (bq / Hq) * H + (bq % Hq) / G;
+    const float* m_row = pm + bq * splits;
+    const float* l_row = pl + bq * splits;
+
+    // 1) common maximum over the non-empty splits
     float mx = -INFINITY;
-    for (int s = 0; s < splits; ++s)
-        if (pl[bq * splits + s] > 0.0f) mx = fmaxf(mx, pm[bq * splits + s]);
-    float acc0 = 0.0f, acc1 = 0.0f, beta = 0.0f, lsum = 0.0f;
-    for (int s = 0; s < splits; ++s) {
-        const long slot = bq * splits + s;
-        const float lw = pl[slot];
-        if (!(lw > 0.0f)) continue;
-        const float sc = expf(pm[slot] - mx);
-        lsum += lw * sc;
-        acc0 += pdelta[slot * kDim + lane] * sc;
-        acc1 += pdelta[slot * kDim + lane + 64] * sc;
-        beta += pbeta[slot * kMaxClusters + lane] * sc;
+    for (int s = tid; s < splits; s += kMergeThreads)
+        if (l_row[s] > 0.0f) mx = fmaxf(mx, m_row[s]);
+    mx = wave_max(mx);
+    if (lane == 0) s_red[wave] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+    __syncthreads();
+
+    // 2) split weights and the normaliser
+    float lsum = 0.0f;
+    for (int s = tid; s < splits; s += kMergeThreads) {
+        const float lw = l_row[s];
+        const float w = lw > 0.0f ? exp2_fast(m_row[s] - mx) : 0.0f;
+        s_w[s] = w;
+        lsum += lw * w;
     }
-    if (vcent != nullptr) {
-        const uint16_t* vc = vcent + bh * vnc * kDim;
-        for (int c = 0; c < vnc; ++c) {
-            const float bc = readlane(beta, c);
-            acc0 += bc * h2f(vc[c * kDim + lane]);
-            acc1 += bc * h2f(vc[c * kDim + lane + 64]);
+    lsum = wave_sum(lsum);
+    if (lane == 0) s_red[wave] = lsum;
+    __syncthreads();
+    lsum = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
+
+    // 3) residual sums: thread = (channel, parity of the split index)
+    {
+        const int c = tid & (kDim - 1), par = tid >> 7;
+        const float* base = pdelta + (bq * splits) * kDim + c;
+        float acc = 0.0f;
+#pragma unroll 4
+        for (int s = par; s < splits; s += 2) acc = fmaf(s_w[s], base[(long)s * kDim], acc);
+        s_acc[par * kDim + c] = acc;
+    }
+    // 4) cluster mass: thread = (cluster, split index mod 4)
+    {
+        const int c = tid & (kMaxClusters - 1), par = tid >> 6;
+        const float* base = pbeta + (bq * splits) * kMaxClusters + c;
+        float acc = 0.0f;
+#pragma unroll 4
+        for (int s = par; s < splits; s += 4) acc = fmaf(s_w[s], base[(long)s * kMaxClusters], acc);
+        s_acc[2 * kDim + par * kMaxClusters + c] = acc;
+    }
+    __syncthreads();
+    // 5) fold sum_c beta_c c_v[c], normalise (threads 0..127: one channel each)
+    if (tid < kDim) {
+        float acc = s_acc[tid] + s_acc[kDim + tid];
+        if (vcent != nullptr) {
+            const uint16_t* vc = vcent + bh * vnc * kDim + tid;
+            const float* bb = s_acc + 2 * kDim;
+            for (int c = 0; c < vnc; ++c) {
+                const float beta = (bb[c] + bb[kMaxClusters + c]) + (bb[2 * kMaxClusters + c] + bb[3 * kMaxClusters + c]);
+                acc = fmaf(beta, h2f(vc[c * kDim]), acc);
+            }
         }
-    }
-    const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
-    out[bq * kDim + lane] = f2h(acc0 * inv);
-    out[bq * kDim + lane + 64] = f2h(acc1 * inv);
-    if (lane == 0) {
-        if (om) om[bq] = mx;
-        if (ol) ol[bq] = lsum;
+        const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
+        out[bq * kDim + tid] = f2h(acc * inv);
+        if (tid == 0) {
+            if (om) om[bq] = mx * kLn2;  // natural-log units, as the reference returns m
+            if (ol) ol[bq] = lsum;
+        }
     }
 }
 
@@ -322,17 +643,23 @@ __global__ void __launch_bounds__(64) merge_recent_kernel(
     out[bq * kDim + lane + 64] = f2h((h2f(comp_out[bq * kDim + lane + 64]) * wc + a1 * wr) * inv);
 }
 
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
 int auto_splits(int B, int H, int T) {
     const long heads = (long)B * H;
-    long s = (2048 + heads - 1) / heads;  // ~8 workgroups per CU over 256 CUs
-    const long cap = T / 32 > 0 ? T / 32 : 1;
+    long s = (1024 + heads - 1) / heads;  // ~4 workgroups (16 waves) per CU over 256 CUs
+    const long cap = T / (kWaves * kTile) > 0 ? T / (kWaves * kTile) : 1;
     if (s > cap) s = cap;
     if (s > kMaxSplits) s = kMaxSplits;
     return (int)(s < 1 ? 1 : s);
 }
 
 int resolve_splits(int B, int H, int T, int splits) {
-    if (splits > 0) return splits < T ? (splits < kMaxSplits ? splits : kMaxSplits) : T;
+    if (splits > 0) {
+        int s = splits < T ? splits : T;
+        return s < kMaxSplits ? s : kMaxSplits;
+    }
     return auto_splits(B, H, T);
 }
 
@@ -340,9 +667,24 @@ int64_t workspace_for(int B, int Hq, int S) {
     return (int64_t)B * Hq * S * (2 + kDim + kMaxClusters) * (int64_t)sizeof(float);
 }
 
-CTensor to_ct(const reskv_ctensor* c) {
-    return CTensor{(const uint16_t*)c->centroids, c->ids, c->payload, c->meta,
-                   (const uint16_t*)c->scale, c->nc, c->format, c->width, c->bits};
+int dfmt_of(const reskv_ctensor* c) {
+    switch (c->format) {
+    case RESKV_FMT_BITMAP: return D_BITMAP;
+    case RESKV_FMT_TILED: return D_TILED;
+    case RESKV_FMT_STRUCT16: return D_STRUCT16;
+    case RESKV_FMT_STRUCT_INT4: return D_SINT4;
+    default: return c->bits == 4 ? D_Q4 : D_Q2;
+    }
+}
+
+int payload_bytes(int f, int width) {
+    switch (f) {
+    case D_BITMAP: case D_TILED: case D_STRUCT16: return 2 * width;
+    case D_SINT4: return 16;
+    case D_Q4: return 64;
+    case D_Q2: return 32;
+    default: return 2 * kDim;
+    }
 }
 
 int check_ct(const reskv_ctensor* c, const char* name) {
@@ -351,7 +693,8 @@ int check_ct(const reskv_ctensor* c, const char* name) {
     RESKV_REQUIRE(c->nc >= 1 && c->nc <= kMaxClusters, "%s: centroid count must be in [1, 64]", name);
     switch (c->format) {
     case RESKV_FMT_BITMAP:
-        RESKV_REQUIRE(c->meta && c->width >= 1 && c->width <= kDim, "%s: bad bitmap tensor", name);
+        RESKV_REQUIRE(c->meta && c->width >= 8 && c->width <= kDim && c->width % 8 == 0,
+                      "%s: bitmap payload width must be a multiple of 8 in [8, 128]", name);
         break;
     case RESKV_FMT_TILED:
         RESKV_REQUIRE(c->meta && c->width % 8 == 0 && c->width >= 8 && c->width < kDim, "%s: bad tiled tensor", name);
@@ -369,21 +712,68 @@ int check_ct(const reskv_ctensor* c, const char* name) {
     default:
         RESKV_REQUIRE(false, "%s: unknown residual format %d", name, c->format);
     }
+    const uintptr_t align = (uintptr_t)c->payload | (uintptr_t)(c->meta ? c->meta : c->payload);
+    RESKV_REQUIRE((align & 15u) == 0, "%s: payload and metadata must be 16-byte aligned", name);
     return 0;
 }
 
-template <int G>
-void launch_partial(dim3 grid, hipStream_t st, const uint16_t* q, const CTensor& k, const CTensor& v,
-                    const float* f, int Hq, int H, int T, int start, int pos, float scaling, int S,
-                    float* pm, float* pl, float* pd, float* pb) {
-    hipLaunchKernelGGL(decode_partial_kernel<G>, grid, dim3(256), 0, st, q, k, v, f, Hq, H, T, start, pos,
-                       scaling, S, pm, pl, pd, pb);
+DTensor to_dt(const reskv_ctensor* c, int f) {
+    return DTensor{(const uint16_t*)c->centroids, c->ids, (const uint8_t*)c->payload, (const uint8_t*)c->meta,
+                   (const uint16_t*)c->scale, c->nc, c->width, payload_bytes(f, c->width)};
 }
 
-int run_decode(const void* q, const CTensor& k, const CTensor& v, const uint16_t* vcent, int vnc,
-               const float* inv_freq, int B, int Hq, int H, int T, int start_pos, int pos_q,
-               float scaling, int splits, void* out, float* m, float* l, void* ws, int64_t ws_bytes,
-               void* stream) {
+template <int F>
+int stage_of(int pb) { return stage_bytes<F>(pb); }
+
+int stage_bytes_rt(int f, int pb) {
+    switch (f) {
+    case D_BITMAP: return stage_of<D_BITMAP>(pb);
+    case D_TILED: return stage_of<D_TILED>(pb);
+    case D_STRUCT16: return stage_of<D_STRUCT16>(pb);
+    case D_SINT4: return stage_of<D_SINT4>(pb);
+    case D_Q4: return stage_of<D_Q4>(pb);
+    case D_Q2: return stage_of<D_Q2>(pb);
+    default: return stage_of<D_DENSE>(pb);
+    }
+}
+
+template <int G, int KF, int VF>
+int launch_g(dim3 grid, size_t shm, hipStream_t st, const DParams& p) {
+    hipLaunchKernelGGL((decode_partial_kernel<G, KF, VF>), grid, dim3(kThreads), shm, st, p);
+    return reskv_host::check_launch("decode_partial_kernel");
+}
+
+template <int KF, int VF>
+int launch_fmt(int G, dim3 grid, size_t shm, hipStream_t st, const DParams& p) {
+    switch (G) {
+    case 1: return launch_g<1, KF, VF>(grid, shm, st, p);
+    case 2: return launch_g<2, KF, VF>(grid, shm, st, p);
+    case 4: return launch_g<4, KF, VF>(grid, shm, st, p);
+    default: return launch_g<8, KF, VF>(grid, shm, st, p);
+    }
+}
+
+int launch_partial(int kf, int vf, int G, dim3 grid, size_t shm, hipStream_t st, const DParams& p) {
+    if (kf == vf) {
+        switch (kf) {
+        case D_BITMAP: return launch_fmt<D_BITMAP, D_BITMAP>(G, grid, shm, st, p);
+        case D_TILED: return launch_fmt<D_TILED, D_TILED>(G, grid, shm, st, p);
+        case D_STRUCT16: return launch_fmt<D_STRUCT16, D_STRUCT16>(G, grid, shm, st, p);
+        case D_SINT4: return launch_fmt<D_SINT4, D_SINT4>(G, grid, shm, st, p);
+        case D_Q4: return launch_fmt<D_Q4, D_Q4>(G, grid, shm, st, p);
+        case D_Q2: return launch_fmt<D_Q2, D_Q2>(G, grid, shm, st, p);
+        default: return launch_fmt<D_DENSE, D_DENSE>(G, grid, shm, st, p);
+        }
+    }
+    if (kf == D_Q4 && vf == D_Q2) return launch_fmt<D_Q4, D_Q2>(G, grid, shm, st, p);
+    if (kf == D_Q2 && vf == D_Q4) return launch_fmt<D_Q2, D_Q4>(G, grid, shm, st, p);
+    RESKV_REQUIRE(false, "K and V residual formats must match (INT4/INT2 may mix)");
+    return 1;
+}
+
+int run_decode(const void* q, int kf, const DTensor& k, int vf, const DTensor& v, const float* inv_freq, int B,
+               int Hq, int H, int T, int start_pos, int pos_q, float scaling, int splits, void* out, float* m,
+               float* l, void* ws, int64_t ws_bytes, void* stream) {
     RESKV_REQUIRE(q && inv_freq && out, "null pointer argument");
     RESKV_REQUIRE(B > 0 && H > 0 && T > 0, "batch, head and token counts must be positive");
     RESKV_REQUIRE(Hq % H == 0, "query heads must be a multiple of KV heads");
@@ -391,22 +781,36 @@ int run_decode(const void* q, const CTensor& k, const CTensor& v, const uint16_t
     RESKV_REQUIRE(G == 1 || G == 2 || G == 4 || G == 8, "supported GQA ratios are 1, 2, 4 and 8");
     const int S = resolve_splits(B, H, T, splits);
     RESKV_REQUIRE(ws != nullptr && ws_bytes >= workspace_for(B, Hq, S), "decode workspace too small");
-    float* pm = (float*)ws;
-    float* pl = pm + (long)B * Hq * S;
-    float* pd = pl + (long)B * Hq * S;
-    float* pb = pd + (long)B * Hq * S * kDim;
+    RESKV_REQUIRE(((uintptr_t)inv_freq & 15u) == 0, "inv_freq must be 16-byte aligned");
+    DParams p{};
+    p.q = (const uint16_t*)q;
+    p.k = k;
+    p.v = v;
+    p.inv_freq = inv_freq;
+    p.Hq = Hq;
+    p.H = H;
+    p.T = T;
+    p.start_pos = start_pos;
+    p.pos_q = pos_q;
+    p.splits = S;
+    p.qscale = scaling * kLog2e;
+    p.stage_k = stage_bytes_rt(kf, k.pb);
+    p.stage_v = stage_bytes_rt(vf, v.pb);
+    const bool cent = kf != D_DENSE;
+    const int merge_bytes = kWaves * G * kPartStride * 4;
+    const int cent_bytes = cent ? k.nc * kDim * 4 : 0;
+    p.region0 = cent_bytes > merge_bytes ? cent_bytes : merge_bytes;
+    const int beta_bytes = cent ? kWaves * G * kMaxClusters * 4 : 0;
+    const size_t shm = (size_t)p.region0 + beta_bytes + (size_t)kWaves * (p.stage_k + p.stage_v);
+    RESKV_REQUIRE(shm <= 65536, "decode LDS requirement %zu exceeds 64 KiB", shm);
+    p.pm = (float*)ws;
+    p.pl = p.pm + (long)B * Hq * S;
+    p.pd = p.pl + (long)B * Hq * S;
+    p.pb = p.pd + (long)B * Hq * S * kDim;
     hipStream_t st = (hipStream_t)stream;
-    dim3 grid(S, H, B);
-    const uint16_t* qq = (const uint16_t*)q;
-    switch (G) {
-    case 1: launch_partial<1>(grid, st, qq, k, v, inv_freq, Hq, H, T, start_pos, pos_q, scaling, S, pm, pl, pd, pb); break;
-    case 2: launch_partial<2>(grid, st, qq, k, v, inv_freq, Hq, H, T, start_pos, pos_q, scaling, S, pm, pl, pd, pb); break;
-    case 4: launch_partial<4>(grid, st, qq, k, v, inv_freq, Hq, H, T, start_pos, pos_q, scaling, S, pm, pl, pd, pb); break;
-    default: launch_partial<8>(grid, st, qq, k, v, inv_freq, Hq, H, T, start_pos, pos_q, scaling, S, pm, pl, pd, pb); break;
-    }
-    if (reskv_host::check_launch("decode_partial_kernel")) return 1;
-    hipLaunchKernelGGL(decode_merge_kernel, dim3(B * Hq), dim3(64), 0, st, pm, pl, pd, pb, vcent, vnc, Hq, H, S,
-                       (uint16_t*)out, m, l);
+    if (launch_partial(kf, vf, G, dim3(S, H, B), shm, st, p)) return 1;
+    hipLaunchKernelGGL(decode_merge_kernel, dim3(B * Hq), dim3(kMergeThreads), 0, st, p.pm, p.pl, p.pd, p.pb,
+                       cent ? v.cent : nullptr, v.nc, Hq, H, S, (uint16_t*)out, m, l);
     return reskv_host::check_launch("decode_merge_kernel");
 }
 
@@ -428,8 +832,9 @@ extern "C" int reskv_decode(const void* q, const reskv_ctensor* k, const reskv_c
                             int pos_q, float scaling, int splits, void* out, float* m, float* l,
                             void* workspace, int64_t workspace_bytes, void* stream) {
     if (check_ct(k, "K") || check_ct(v, "V")) return 1;
-    return run_decode(q, to_ct(k), to_ct(v), (const uint16_t*)v->centroids, v->nc, inv_freq, B, Hq, H, T,
-                      start_pos, pos_q, scaling, splits, out, m, l, workspace, workspace_bytes, stream);
+    const int kf = dfmt_of(k), vf = dfmt_of(v);
+    return run_decode(q, kf, to_dt(k, kf), vf, to_dt(v, vf), inv_freq, B, Hq, H, T, start_pos, pos_q, scaling,
+                      splits, out, m, l, workspace, workspace_bytes, stream);
 }
 
 extern "C" int reskv_decode_dense(const void* q, const void* k, const void* v, const float* inv_freq,
@@ -437,10 +842,11 @@ extern "C" int reskv_decode_dense(const void* q, const void* k, const void* v, c
                                   int splits, void* out, float* m, float* l, void* workspace,
                                   int64_t workspace_bytes, void* stream) {
     RESKV_REQUIRE(k && v, "null K/V pointer");
-    const CTensor kd{nullptr, nullptr, k, nullptr, nullptr, 1, kFmtDense, kDim, 16};
-    const CTensor vd{nullptr, nullptr, v, nullptr, nullptr, 1, kFmtDense, kDim, 16};
-    return run_decode(q, kd, vd, nullptr, 0, inv_freq, B, Hq, H, T, start_pos, pos_q, scaling, splits, out, m, l,
-                      workspace, workspace_bytes, stream);
+    RESKV_REQUIRE((((uintptr_t)k | (uintptr_t)v) & 15u) == 0, "K and V must be 16-byte aligned");
+    const DTensor kd{nullptr, nullptr, (const uint8_t*)k, nullptr, nullptr, 1, kDim, 2 * kDim};
+    const DTensor vd{nullptr, nullptr, (const uint8_t*)v, nullptr, nullptr, 1, kDim, 2 * kDim};
+    return run_decode(q, D_DENSE, kd, D_DENSE, vd, inv_freq, B, Hq, H, T, start_pos, pos_q, scaling, splits, out,
+                      m, l, workspace, workspace_bytes, stream);
 }
 
 extern "C" int reskv_merge_recent_scores(const void* comp_out, const float* comp_m, const float* comp_l,
