@@ -183,6 +183,105 @@ def measure_dense(torch, b, t, layers, steps, warmup, device):
             "frac": nbytes / per_call / HBM_PEAK, "distinct_caches": n}
 
 
+def measure_encoders(torch, device, reps=20):
+    """prefill compression of one layer, B=1, 8 KV heads, T=8192.
+
+    K-means (32 clusters, 10 iterations) over K and over V, then the residual
+    encoders at 75% sparsity (structured 4:16 and forced-unstructured bitmaps).
+    Encoder bytes = x + ids + centroid table read, payload + metadata written.
+    K-means work = 2*T*C*D FLOP per head per iteration for the distances.
+    """
+    from reskv_amd._extension import load_extension
+    from reskv_amd.compression import cluster
+
+    ext = load_extension("compression")
+    g = torch.Generator(device=device).manual_seed(1)
+    b, h, t = 1, HK, T
+    scale = torch.exp(torch.randn(1, h, 1, D, device=device, generator=g))
+    k = (torch.randn(b, h, t, D, device=device, generator=g) * scale).half()
+    v = torch.randn(b, h, t, D, device=device, generator=g).half()
+
+    def timed(fn, n=reps):
+        fn()
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(n):
+            fn()
+        e.record()
+        e.synchronize()
+        return s.elapsed_time(e) / n * 1e3  # us
+
+    out = {}
+    kc, ki = cluster(k, 32, 10)
+    vc, vi = cluster(v, 32, 10, value=True)
+    us_k = timed(lambda: cluster(k, 32, 10), max(3, reps // 4))
+    us_v = timed(lambda: cluster(v, 32, 10, value=True), max(3, reps // 4))
+    flop = 2.0 * t * 32 * D * h * 10
+    out["kmeans"] = {"us_k": us_k, "us_v": us_v, "tflops_k": flop / us_k / 1e6, "tflops_v": flop / us_v / 1e6,
+                     "iterations": 10, "clusters": 32}
+    n_in = b * h * t * (D * 2 + 4) + b * h * 32 * D * 2
+    us = timed(lambda: (ext.compress_fp16(k, kc, ki, 32, True), ext.compress_fp16(v, vc, vi, 32, True)))
+    n_out = b * h * t * (32 * 2 + 16)
+    out["structured_fp16_75"] = {"us_kv": us, "GBps": 2 * (n_in + n_out) / us / 1e3,
+                                 "frac": 2 * (n_in + n_out) / us / 1e3 / (HBM_PEAK / 1e9)}
+    us = timed(lambda: (ext.compress_bitmap(k, kc, ki, 32), ext.compress_bitmap(v, vc, vi, 32)))
+    n_out = b * h * t * (32 * 2 + 16)
+    out["bitmap_fp16_75"] = {"us_kv": us, "GBps": 2 * (n_in + n_out) / us / 1e3,
+                             "frac": 2 * (n_in + n_out) / us / 1e3 / (HBM_PEAK / 1e9)}
+    del k, v
+    torch.cuda.empty_cache()
+    return out
+
+
+def measure_quantized(torch, device, steps, layers=32):
+    """INT4 / INT2 unstructured residuals at T=16384, B=8, 50% sparsity."""
+    out = {}
+    for bits in (4, 2):
+        r = measure_point_bits(torch, 8, 16384, bits, layers, steps, device)
+        out[f"int{bits}"] = {k: r[k] for k in ("us_per_layer_step", "achieved_GBps", "frac", "splits")}
+    return out
+
+
+def measure_point_bits(torch, b, t, bits, layers, steps, device):
+    from reskv_amd import ResKVKernelConfig, attention, compress
+    from reskv_amd.tensors import CompressedKV, CompressedTensor
+
+    cfg = ResKVKernelConfig(sparsity=0.5, bits=bits)
+    g = torch.Generator(device=device).manual_seed(3)
+    k = torch.randn(b, HK, t, D, device=device, dtype=torch.float16, generator=g) * 0.5
+    v = torch.randn(b, HK, t, D, device=device, dtype=torch.float16, generator=g) * 0.5
+    kc = torch.randn(b, HK, 32, D, device=device, dtype=torch.float16, generator=g) * 0.1
+    vc = torch.randn(b, HK, 32, D, device=device, dtype=torch.float16, generator=g) * 0.1
+    ki = torch.randint(32, (b, HK, t), device=device, dtype=torch.int32, generator=g)
+    vi = torch.randint(32, (b, HK, t), device=device, dtype=torch.int32, generator=g)
+    base = compress(k, v, cfg, clustering=((kc, ki), (vc, vi)))
+    del k, v
+
+    def clone(ct):
+        return CompressedTensor(ct.centroids.clone(), ct.cluster_ids.clone(), ct.payload.clone(), None,
+                                ct.scale.clone(), ct.plan)
+
+    caches = [base] + [CompressedKV(clone(base.key), clone(base.value)) for _ in range(layers - 1)]
+    q = torch.randn(b, HQ, 1, D, device=device, dtype=torch.float16, generator=g)
+    freq = (500000.0 ** (-torch.arange(64, device=device).float() / 64)).float()
+
+    def step():
+        for c in caches:
+            attention(q, c, position=t, inv_freq=freq)
+
+    secs = graph_time(torch, step, steps, 2)
+    per_call = secs / (steps * layers)
+    nbytes = algorithmic_bytes(base.key.plan, b, t, 32, 32)
+    from reskv_amd import _lib
+
+    nsplit = _lib.lib().reskv_decode_splits(b, HQ, HK, t, 0)
+    del caches
+    torch.cuda.empty_cache()
+    return {"us_per_layer_step": per_call * 1e6, "achieved_GBps": nbytes / per_call / 1e9,
+            "frac": nbytes / per_call / HBM_PEAK, "splits": nsplit}
+
+
 def cpu_baseline(seconds_budget, t, sparsity):
     """numpy oracle decode (reconstruct + float64 attention) on one batch element."""
     import numpy as np
@@ -278,6 +377,12 @@ def main():
             d = measure_dense(torch, b, args.seq_len, args.layers, max(5, args.steps // 2), 2, device)
             dense.append(d)
             print(json.dumps({"dense": d}), flush=True)
+    encode = quant = None
+    if not args.no_sweep:
+        encode = measure_encoders(torch, device)
+        print(json.dumps({"encode": encode}), flush=True)
+        quant = measure_quantized(torch, device, max(5, args.steps // 2))
+        print(json.dumps({"quantized": quant}), flush=True)
     dense_b = next((d for d in dense if d["batch"] == args.batch), None)
     if dense_b is None:
         dense_b = measure_dense(torch, args.batch, args.seq_len, args.layers, max(5, args.steps // 2), 2, device)
@@ -310,6 +415,8 @@ def main():
             "parallelism": "single GPU",
             "sweep": sweep,
             "dense_sweep": [{k: d[k] for k in ("batch", "us_per_layer_step", "frac")} for d in dense],
+            "config1_prefill_compression": encode,
+            "config3_quantized_decode_b8_t16384": quant,
         },
         "roofline": {
             "bound": "hbm", "achieved": r["achieved_GBps"], "peak": HBM_PEAK / 1e9, "unit": "GB/s",

@@ -30,7 +30,9 @@ using namespace reskv;
 namespace {
 
 // residual formats as the kernels see them (the two quantised widths split)
-enum DFmt { D_BITMAP = 0, D_TILED, D_STRUCT16, D_SINT4, D_Q4, D_Q2, D_DENSE };
+// (_W: the same layout with payload rows wider than 128 bytes, i.e. nnz > 64,
+// which needs more prefetch registers per lane)
+enum DFmt { D_BITMAP = 0, D_TILED, D_STRUCT16, D_SINT4, D_Q4, D_Q2, D_DENSE, D_BITMAP_W, D_TILED_W };
 
 constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * kWave;
@@ -43,8 +45,10 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 
 template <int F> struct Traits;
-template <> struct Traits<D_BITMAP> { static constexpr int MB = 16, PQ = 4; static constexpr bool SC = false, CENT = true; };
-template <> struct Traits<D_TILED> { static constexpr int MB = 16, PQ = 4; static constexpr bool SC = false, CENT = true; };
+template <> struct Traits<D_BITMAP> { static constexpr int MB = 16, PQ = 2; static constexpr bool SC = false, CENT = true; };
+template <> struct Traits<D_TILED> { static constexpr int MB = 16, PQ = 2; static constexpr bool SC = false, CENT = true; };
+template <> struct Traits<D_BITMAP_W> { static constexpr int MB = 16, PQ = 4; static constexpr bool SC = false, CENT = true; };
+template <> struct Traits<D_TILED_W> { static constexpr int MB = 16, PQ = 4; static constexpr bool SC = false, CENT = true; };
 template <> struct Traits<D_STRUCT16> { static constexpr int MB = 16, PQ = 1; static constexpr bool SC = false, CENT = true; };
 template <> struct Traits<D_SINT4> { static constexpr int MB = 8, PQ = 1; static constexpr bool SC = true, CENT = true; };
 template <> struct Traits<D_Q4> { static constexpr int MB = 0, PQ = 1; static constexpr bool SC = true, CENT = true; };
@@ -67,7 +71,7 @@ struct DParams {
     int Hq, H, T, start_pos, pos_q, splits;
     float qscale;  // scaling * log2(e): scores come out in the log2 domain
     int stage_k, stage_v;  // LDS stage bytes per wave for K and V
-    int region0;           // bytes of the centroid / merge region
+    int beta_off, lut_off, p_off, stage_off;  // LDS byte offsets (region 0 holds centroids / merge records)
     float* pm;
     float* pl;
     float* pd;
@@ -164,48 +168,78 @@ __host__ __device__ constexpr int stage_bytes(int pb) {
 // ---------------------------------------------------------------------------
 // residual decoders (LDS stage -> 8 fp32 values of this lane's channels)
 // r[0..3] = channels 4i..4i+3, r[4..7] = channels 64+4i..64+4i+3
+//
+// FP16 formats: the kept values of a lane's 4-channel run are consecutive in
+// the payload row, starting at rank `base`.  The 8-byte window at `base` is
+// fetched with two dword reads plus an alignbit, and one v_perm per channel
+// pair scatters the window's halves onto the kept channels (zeros elsewhere).
+// The permute selectors depend only on the run's 4-bit keep pattern and come
+// from a 16-entry table in LDS (one table for MSB-first bitmaps, one for
+// LSB-first tile masks).
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ float lds_h(const uint16_t* p, int idx) { return h2f(p[idx]); }
+constexpr int kLutWords = 64;  // [msb|lsb][pattern][lo|hi]
 
-// 4 channels of a 16-bit LSB-first tile mask: nib bit j = channel j; values at base + rank
-__device__ __forceinline__ void expand4(uint32_t nib, int base, const uint16_t* p, float* r) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int idx = base + __builtin_popcount(nib & ((1u << j) - 1u));
-        r[j] = ((nib >> j) & 1u) ? lds_h(p, idx) : 0.0f;
+// v_perm selector bytes placing window halves on channels 0..3 of a run
+// (byte 12 selects zero).  msb: pattern bit 3-j = channel j (bitmaps);
+// otherwise bit j = channel j (tile masks).
+__host__ __device__ constexpr uint32_t perm_selector(uint32_t v, bool msb, int half) {
+    uint32_t sel = 0;
+    for (int jj = 0; jj < 2; ++jj) {
+        const int j = 2 * half + jj;
+        const bool kept = msb ? ((v >> (3 - j)) & 1u) : ((v >> j) & 1u);
+        const uint32_t rank = msb ? (uint32_t)__builtin_popcount(v >> (4 - j))
+                                  : (uint32_t)__builtin_popcount(v & ((1u << j) - 1u));
+        const uint32_t b0 = kept ? 2 * rank : 12u, b1 = kept ? 2 * rank + 1 : 12u;
+        sel |= (b0 | (b1 << 8)) << (16 * jj);
     }
+    return sel;
+}
+
+__device__ __forceinline__ float half_lo(uint32_t w) { return h2f((uint16_t)(w & 0xFFFFu)); }
+__device__ __forceinline__ float half_hi(uint32_t w) { return h2f((uint16_t)(w >> 16)); }
+
+// Kept values of one 4-channel run, as fp32: window of the payload row at
+// rank `base`, scattered by the pattern's selectors.
+__device__ __forceinline__ void expand_run(const uint8_t* row, int base, const uint32_t* lut, uint32_t v,
+                                           float* r) {
+    const uint32_t* dw = reinterpret_cast<const uint32_t*>(row) + (base >> 1);
+    const uint32_t d0 = dw[0], d1 = dw[1], d2 = dw[2];
+    const uint32_t sh = (uint32_t)(base & 1) * 16u;
+    const uint32_t w0 = __builtin_amdgcn_alignbit(d1, d0, sh);
+    const uint32_t w1 = __builtin_amdgcn_alignbit(d2, d1, sh);
+    const uint2 sel = *reinterpret_cast<const uint2*>(lut + 2 * v);
+    const uint32_t lo = __builtin_amdgcn_perm(w1, w0, sel.x);
+    const uint32_t hi = __builtin_amdgcn_perm(w1, w0, sel.y);
+    r[0] = half_lo(lo);
+    r[1] = half_hi(lo);
+    r[2] = half_lo(hi);
+    r[3] = half_hi(hi);
 }
 
 template <int F>
-__device__ __forceinline__ void decode_res(const uint8_t* st, int tok, int pb, int width, int li, float* r) {
+__device__ __forceinline__ void decode_res(const uint8_t* st, int tok, int pb, int width, int li,
+                                           const uint32_t* lut, float* r) {
     using Tr = Traits<F>;
     const uint8_t* payb = st + tok * pb;
-    const uint16_t* p16 = reinterpret_cast<const uint16_t*>(payb);
     const uint8_t* meta = st + kTile * pb + tok * Tr::MB;
-    if constexpr (F == D_BITMAP) {
+    if constexpr (F == D_BITMAP || F == D_BITMAP_W) {
         // channel d <-> bit (63 - d % 64) of word d / 64; value index = rank (reference.py:22-26)
         const uint4 m = *reinterpret_cast<const uint4*>(meta);
         const uint64_t w0 = (uint64_t)m.x | ((uint64_t)m.y << 32);
         const uint64_t w1 = (uint64_t)m.z | ((uint64_t)m.w << 32);
         const int sh = 60 - 4 * li;
         const uint32_t na = (uint32_t)(w0 >> sh) & 15u, nb = (uint32_t)(w1 >> sh) & 15u;
-        // bits above this lane's nibble: (w >> 1) >> (63 - 4i) keeps every shift below 64
+        // bits above this lane's run: (w >> 1) >> (63 - 4i) keeps every shift below 64
         const int hi = 63 - 4 * li;
         const int ba = li ? __builtin_popcountll((w0 >> 1) >> hi) : 0;
         const int bb = __builtin_popcountll(w0) + (li ? __builtin_popcountll((w1 >> 1) >> hi) : 0);
-        // MSB-first: channel 4i+j is nibble bit 3-j; earlier channels are the higher bits
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int ia = ba + __builtin_popcount(na >> (4 - j));
-            const int ib = bb + __builtin_popcount(nb >> (4 - j));
-            r[j] = ((na >> (3 - j)) & 1u) ? lds_h(p16, ia) : 0.0f;
-            r[4 + j] = ((nb >> (3 - j)) & 1u) ? lds_h(p16, ib) : 0.0f;
-        }
-    } else if constexpr (F == D_TILED || F == D_STRUCT16) {
+        expand_run(payb, ba, lut, na, r);
+        expand_run(payb, bb, lut, nb, r + 4);
+    } else if constexpr (F == D_TILED || F == D_TILED_W || F == D_STRUCT16) {
         // word w = code(tile 2w) | code(tile 2w+1) << 16 (reference.py:36-47)
         const uint4 m = *reinterpret_cast<const uint4*>(meta);
         const uint32_t mw[4] = {m.x, m.y, m.z, m.w};
-        const int per_tile = F == D_TILED ? (width >> 3) : 4;
+        const int per_tile = F == D_STRUCT16 ? 4 : (width >> 3);
         const int sub = li & 3;
 #pragma unroll
         for (int half = 0; half < 2; ++half) {
@@ -220,7 +254,7 @@ __device__ __forceinline__ void decode_res(const uint8_t* st, int tok, int pb, i
             }
             const uint32_t nib = (code >> (4 * sub)) & 15u;
             const int base = tile * per_tile + __builtin_popcount(code & ((1u << (4 * sub)) - 1u));
-            expand4(nib, base, p16, r + 4 * half);
+            expand_run(payb, base, lut + 32, nib, r + 4 * half);
         }
     } else if constexpr (F == D_SINT4) {
         // 1 of 4 per subgroup: 2-bit position, signed nibble code, fp16 scale (reference.py:27-35)
@@ -232,8 +266,8 @@ __device__ __forceinline__ void decode_res(const uint8_t* st, int tok, int pb, i
         for (int half = 0; half < 2; ++half) {
             const int grp = li + 16 * half;
             const uint32_t sel = ((half ? qm.y : qm.x) >> (2 * li)) & 3u;
-            const int code = (int)((qw[grp >> 3] >> (4 * (grp & 7))) & 15u);
-            const float val = (float)((code ^ 8) - 8) * s;
+            const int code = (int)__builtin_amdgcn_sbfe((int)qw[grp >> 3], 4 * (grp & 7), 4);  // typed unsigned
+            const float val = (float)code * s;
 #pragma unroll
             for (int j = 0; j < 4; ++j) r[4 * half + j] = (uint32_t)j == sel ? val : 0.0f;
         }
@@ -241,30 +275,28 @@ __device__ __forceinline__ void decode_res(const uint8_t* st, int tok, int pb, i
         // signed codes, channel d in word d / (32/bits) at bit (d % (32/bits)) * bits (reference.py:17-21)
         constexpr int bits = F == D_Q4 ? 4 : 2;
         constexpr int per_word = 32 / bits;
-        constexpr int sign = 1 << (bits - 1);
         const uint32_t* qw = reinterpret_cast<const uint32_t*>(payb);
         const float s = reinterpret_cast<const float*>(st + kTile * pb + kTile * 4)[tok];
 #pragma unroll
         for (int half = 0; half < 2; ++half) {
             const int d0 = 4 * li + 64 * half;
-            const uint32_t w = qw[d0 / per_word] >> ((d0 % per_word) * bits);
+            const int w = (int)qw[d0 / per_word];
+            const int off = (d0 % per_word) * bits;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int code = (int)((w >> (j * bits)) & (uint32_t)((1 << bits) - 1));
-                r[4 * half + j] = (float)((code ^ sign) - sign) * s;
-            }
+            for (int j = 0; j < 4; ++j) r[4 * half + j] = (float)(int)__builtin_amdgcn_sbfe(w, off + j * bits, bits) * s;
         }
     } else {  // dense fp16 rows
+        const uint16_t* p16 = reinterpret_cast<const uint16_t*>(payb);
         const uint2 a = *reinterpret_cast<const uint2*>(p16 + 4 * li);
         const uint2 b = *reinterpret_cast<const uint2*>(p16 + 64 + 4 * li);
-        r[0] = h2f((uint16_t)(a.x & 0xFFFFu));
-        r[1] = h2f((uint16_t)(a.x >> 16));
-        r[2] = h2f((uint16_t)(a.y & 0xFFFFu));
-        r[3] = h2f((uint16_t)(a.y >> 16));
-        r[4] = h2f((uint16_t)(b.x & 0xFFFFu));
-        r[5] = h2f((uint16_t)(b.x >> 16));
-        r[6] = h2f((uint16_t)(b.y & 0xFFFFu));
-        r[7] = h2f((uint16_t)(b.y >> 16));
+        r[0] = half_lo(a.x);
+        r[1] = half_hi(a.x);
+        r[2] = half_lo(a.y);
+        r[3] = half_hi(a.y);
+        r[4] = half_lo(b.x);
+        r[5] = half_hi(b.x);
+        r[6] = half_lo(b.y);
+        r[7] = half_hi(b.y);
     }
 }
 
@@ -278,14 +310,34 @@ __device__ __forceinline__ int clamp_id(int id, int nc) { return id < 0 ? 0 : (i
 __device__ __forceinline__ float rows_max(float v) {
     return fmaxf(fmaxf(readlane(v, 0), readlane(v, 16)), fmaxf(readlane(v, 32), readlane(v, 48)));
 }
-__device__ __forceinline__ float rows_sum(float v) {
-    return (readlane(v, 0) + readlane(v, 16)) + (readlane(v, 32) + readlane(v, 48));
-}
 // sum over the four rows, result in every lane (lanes i, i+16, i+32, i+48)
 __device__ __forceinline__ float cross_rows_sum(float v) {
     v += __shfl_xor(v, 16);
     v += __shfl_xor(v, 32);
     return v;
+}
+
+// ---------------------------------------------------------------------------
+// RoPE by recurrence.  A lane keeps (C, S) = cos/sin of the exact angle p*f of
+// its row's current position p (advanced by 4 positions per step with
+// precomputed cos/sin of 4f).  The angle the reference uses is hi = fl32(p*f);
+// e = p*f - hi is exact (one FMA), and cos(hi) = C + e*S, sin(hi) = S - e*C to
+// well below fp32 resolution (|e| <= ulp(hi)/2, so e^2 is negligible).
+// ---------------------------------------------------------------------------
+struct Rope {
+    float C[4], S[4], c4[4], s4[4];
+};
+
+__device__ __forceinline__ void rope_anchor(Rope& R, const float* f, float pos) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const float hi = __fmul_rn(pos, f[j]);
+        const float e = __builtin_fmaf(pos, f[j], -hi);
+        float sn, cs;
+        rope_sincos_fast(hi, sn, cs);
+        R.C[j] = __builtin_fmaf(-e, sn, cs);
+        R.S[j] = __builtin_fmaf(e, cs, sn);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -296,19 +348,24 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
     extern __shared__ __align__(16) uint8_t smem[];
     using KT = Traits<KF>;
     using VT = Traits<VF>;
+    constexpr int NV = kSteps * G;             // softmax values of one row per tile
+    constexpr int NVL = (NV + 15) / 16;        // values per lane
     const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
     const long bh = (long)b * P.H + h;
-    const int t0 = (int)(((long)split * P.T) / P.splits);
-    const int t1 = (int)(((long)(split + 1) * P.T) / P.splits);
+    const int s0 = (int)(((long)split * P.T) / P.splits);
+    const int s1 = (int)(((long)(split + 1) * P.T) / P.splits);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int row = lane >> 4, li = lane & 15;
+    // this wave's contiguous share of the split
+    const int t0 = s0 + (int)(((long)wave * (s1 - s0)) / kWaves);
+    const int t1 = s0 + (int)(((long)(wave + 1) * (s1 - s0)) / kWaves);
 
-    float* s_cent = reinterpret_cast<float*>(smem);                       // region 0
-    float* s_beta = reinterpret_cast<float*>(smem + P.region0);            // [wave][G][64]
-    const int beta_bytes = KT::CENT ? kWaves * G * kMaxClusters * 4 : 0;
-    uint8_t* st_k = smem + P.region0 + beta_bytes + wave * (P.stage_k + P.stage_v);
+    float* s_cent = reinterpret_cast<float*>(smem);                          // region 0
+    float* my_beta = reinterpret_cast<float*>(smem + P.beta_off) + wave * G * kMaxClusters;
+    uint32_t* s_lut = reinterpret_cast<uint32_t*>(smem + P.lut_off);
+    float* my_p = reinterpret_cast<float*>(smem + P.p_off) + wave * kRows * NV;
+    uint8_t* st_k = smem + P.stage_off + wave * (P.stage_k + P.stage_v);
     uint8_t* st_v = st_k + P.stage_k;
-    float* my_beta = s_beta + wave * G * kMaxClusters;
 
     if constexpr (KT::CENT) {
         const uint16_t* kc = P.k.cent + bh * P.k.nc * kDim;
@@ -316,22 +373,30 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
 #pragma unroll
         for (int g = 0; g < G; ++g) my_beta[g * kMaxClusters + lane] = 0.0f;
     }
+    if (threadIdx.x < kLutWords) {
+        const uint32_t t = threadIdx.x;
+        s_lut[t] = perm_selector((t >> 1) & 15u, t < 32, (int)(t & 1));
+    }
 
     // rotated, pre-scaled query: qa = channels 4i+j, qb = channels 64+4i+j
     const float4 fq = *reinterpret_cast<const float4*>(P.inv_freq + 4 * li);
     const float freq[4] = {fq.x, fq.y, fq.z, fq.w};
     float qa[G][4], qb[G][4];
+    Rope R;
     {
         float sn[4], cs[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) rope_sincos_fast(__fmul_rn((float)P.pos_q, freq[j]), sn[j], cs[j]);
+        for (int j = 0; j < 4; ++j) {
+            rope_sincos_fast(__fmul_rn((float)P.pos_q, freq[j]), sn[j], cs[j]);
+            rope_sincos_fast(4.0f * freq[j], R.s4[j], R.c4[j]);  // 4f is exact in fp32
+        }
 #pragma unroll
         for (int g = 0; g < G; ++g) {
             const uint16_t* qr = P.q + ((long)b * P.Hq + (long)h * G + g) * kDim;
             const uint2 ua = *reinterpret_cast<const uint2*>(qr + 4 * li);
             const uint2 ub = *reinterpret_cast<const uint2*>(qr + 64 + 4 * li);
-            const float a[4] = {h2f(ua.x & 0xFFFFu), h2f(ua.x >> 16), h2f(ua.y & 0xFFFFu), h2f(ua.y >> 16)};
-            const float c[4] = {h2f(ub.x & 0xFFFFu), h2f(ub.x >> 16), h2f(ub.y & 0xFFFFu), h2f(ub.y >> 16)};
+            const float a[4] = {half_lo(ua.x), half_hi(ua.x), half_lo(ua.y), half_hi(ua.y)};
+            const float c[4] = {half_lo(ub.x), half_hi(ub.x), half_lo(ub.y), half_hi(ub.y)};
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 qa[g][j] = (a[j] * cs[j] - c[j] * sn[j]) * P.qscale;
@@ -340,37 +405,49 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
         }
     }
 
-    float m[G], l[G], dl[G][8];
+    // this lane's softmax values: v = li + 16k -> (step v / G, head v % G)
+    int vs[NVL], vg[NVL];
+    bool vown[NVL];
+#pragma unroll
+    for (int k = 0; k < NVL; ++k) {
+        const int v = li + 16 * k;
+        vown[k] = v < NV;
+        vs[k] = (v % NV) / G;
+        vg[k] = (v % NV) % G;
+    }
+
+    float m[G], dl[G][8], lv[NVL];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
         m[g] = -INFINITY;
-        l[g] = 0.0f;
 #pragma unroll
         for (int j = 0; j < 8; ++j) dl[g][j] = 0.0f;
     }
+#pragma unroll
+    for (int k = 0; k < NVL; ++k) lv[k] = 0.0f;
     __syncthreads();
 
     const int ntiles = (t1 - t0 + kTile - 1) / kTile;
     Prefetch<KF> pk;
     Prefetch<VF> pv;
-    if (wave < ntiles) {
-        const int tb = t0 + wave * kTile;
-        const int n = min(kTile, t1 - tb);
-        prefetch<KF>(P.k, bh * P.T + tb, n, lane, pk);
-        prefetch<VF>(P.v, bh * P.T + tb, n, lane, pv);
+    if (ntiles > 0) {
+        const int n = min(kTile, t1 - t0);
+        prefetch<KF>(P.k, bh * P.T + t0, n, lane, pk);
+        prefetch<VF>(P.v, bh * P.T + t0, n, lane, pv);
     }
-    for (int tile = wave; tile < ntiles; tile += kWaves) {
+    for (int tile = 0; tile < ntiles; ++tile) {
         const int tb = t0 + tile * kTile;
         const int n = min(kTile, t1 - tb);
         stage_store<KF>(pk, st_k, P.k.pb, lane);
         stage_store<VF>(pv, st_v, P.v.pb, lane);
         wave_sync();
-        if (tile + kWaves < ntiles) {
-            const int tb2 = tb + kWaves * kTile;
+        if (tile + 1 < ntiles) {
+            const int tb2 = tb + kTile;
             const int n2 = min(kTile, t1 - tb2);
             prefetch<KF>(P.k, bh * P.T + tb2, n2, lane, pk);
             prefetch<VF>(P.v, bh * P.T + tb2, n2, lane, pv);
         }
+        if ((tile & 7) == 0) rope_anchor(R, freq, (float)(P.start_pos + tb + row));
 
         // ---- scores of the tile's 16 tokens (log2 domain) ----
         float sc[G][kSteps];
@@ -378,7 +455,7 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
         for (int s = 0; s < kSteps; ++s) {
             const int tok = kRows * s + row;
             float kr[8];
-            decode_res<KF>(st_k, tok, P.k.pb, P.k.width, li, kr);
+            decode_res<KF>(st_k, tok, P.k.pb, P.k.width, li, s_lut, kr);
             if constexpr (KT::CENT) {
                 const int kid = clamp_id(stage_id<KF>(st_k, P.k.pb, tok), P.k.nc);
                 const float4 ca = *reinterpret_cast<const float4*>(s_cent + kid * kDim + 4 * li);
@@ -390,10 +467,15 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
             float xa[4], xb[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                float sn, cs;
-                rope_sincos_fast(__fmul_rn(pos, freq[j]), sn, cs);
+                const float hi = __fmul_rn(pos, freq[j]);
+                const float e = __builtin_fmaf(pos, freq[j], -hi);
+                const float cs = __builtin_fmaf(e, R.S[j], R.C[j]);
+                const float sn = __builtin_fmaf(-e, R.C[j], R.S[j]);
                 xa[j] = kr[j] * cs - kr[4 + j] * sn;
                 xb[j] = kr[4 + j] * cs + kr[j] * sn;
+                const float nc = R.C[j] * R.c4[j] - R.S[j] * R.s4[j];
+                R.S[j] = R.S[j] * R.c4[j] + R.C[j] * R.s4[j];
+                R.C[j] = nc;
             }
             const bool valid = tok < n;
 #pragma unroll
@@ -406,7 +488,7 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
             }
         }
 
-        // ---- online softmax over the tile ----
+        // ---- online softmax over the tile: one exponential per lane value ----
         bool grow = false;
         float mnew[G];
 #pragma unroll
@@ -421,52 +503,60 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
 #pragma unroll
             for (int g = 0; g < G; ++g) {
                 const float alpha = exp2_fast(m[g] - mnew[g]);  // 0 on the first tile
-                l[g] *= alpha;
 #pragma unroll
                 for (int j = 0; j < 8; ++j) dl[g][j] *= alpha;
                 if constexpr (KT::CENT) my_beta[g * kMaxClusters + lane] *= alpha;
+#pragma unroll
+                for (int k = 0; k < NVL; ++k) lv[k] = vg[k] == g ? lv[k] * alpha : lv[k];
                 m[g] = mnew[g];
             }
-            wave_sync();
         }
-        float p[G][kSteps];
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
+        for (int k = 0; k < NVL; ++k) {
+            float pick = sc[0][0], mg = m[0];
 #pragma unroll
-            for (int s = 0; s < kSteps; ++s) {
-                p[g][s] = exp2_fast(sc[g][s] - m[g]);
-                l[g] += p[g][s];
+            for (int g = 0; g < G; ++g) {
+                mg = vg[k] == g ? m[g] : mg;
+#pragma unroll
+                for (int s = 0; s < kSteps; ++s) pick = (vs[k] == s && vg[k] == g) ? sc[g][s] : pick;
+            }
+            const float pk_ = exp2_fast(pick - mg);
+            if (vown[k]) {
+                lv[k] += pk_;
+                my_p[row * NV + li + 16 * k] = pk_;
+                if constexpr (VT::CENT) {
+                    const int vid = clamp_id(stage_id<VF>(st_v, P.v.pb, kRows * vs[k] + row), P.v.nc);
+                    atomicAdd(&my_beta[vg[k] * kMaxClusters + vid], pk_);
+                }
             }
         }
+        wave_sync();
 
-        // ---- values: residual sums and cluster mass ----
+        // ---- values: residual sums ----
 #pragma unroll
         for (int s = 0; s < kSteps; ++s) {
             const int tok = kRows * s + row;
             float vr[8];
-            decode_res<VF>(st_v, tok, P.v.pb, P.v.width, li, vr);
+            decode_res<VF>(st_v, tok, P.v.pb, P.v.width, li, s_lut, vr);
+            float pg[G];
+#pragma unroll
+            for (int g = 0; g < G; ++g) pg[g] = my_p[row * NV + s * G + g];
 #pragma unroll
             for (int g = 0; g < G; ++g)
 #pragma unroll
-                for (int j = 0; j < 8; ++j) dl[g][j] = fmaf(p[g][s], vr[j], dl[g][j]);
-            if constexpr (VT::CENT) {
-                if (li < G) {
-                    float pg = p[0][s];
-#pragma unroll
-                    for (int g = 1; g < G; ++g) pg = li == g ? p[g][s] : pg;
-                    const int vid = clamp_id(stage_id<VF>(st_v, P.v.pb, tok), P.v.nc);
-                    atomicAdd(&my_beta[li * kMaxClusters + vid], pg);
-                }
-            }
+                for (int j = 0; j < 8; ++j) dl[g][j] = fmaf(pg[g], vr[j], dl[g][j]);
         }
-        wave_sync();  // stage reads done before the next tile overwrites it
+        wave_sync();  // stage and p reads done before the next tile overwrites them
     }
 
     // ---- fold the four rows, then merge the waves through LDS ----
     float lt[G];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-        lt[g] = rows_sum(l[g]);
+        float acc = 0.0f;
+#pragma unroll
+        for (int k = 0; k < NVL; ++k) acc += (vown[k] && vg[k] == g) ? lv[k] : 0.0f;
+        lt[g] = wave_sum(acc);
 #pragma unroll
         for (int j = 0; j < 8; ++j) dl[g][j] = cross_rows_sum(dl[g][j]);
     }
@@ -521,8 +611,10 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
 }
 
 // One workgroup (256 threads) per (batch, query head) combines the split
-// partials (log2 domain).  Threads stride over the splits, so every global load
-// of the reduction is independent and many are in flight at once.
+// partials (log2 domain).  The residual sums are read as float4 by 8 groups of
+// 32 threads (split s goes to group s % 8), the cluster masses by 16 groups of
+// 16 threads, so a thread keeps at most S/8 independent loads in flight;
+// the groups are then reduced through LDS.
 constexpr int kMergeThreads = 256;
 
 __global__ void __launch_bounds__(kMergeThreads) decode_merge_kernel(
@@ -531,7 +623,8 @@ __global__ void __launch_bounds__(kMergeThreads) decode_merge_kernel(
     int splits, uint16_t* __restrict__ out, float* __restrict__ om, float* __restrict__ ol) {
     __shared__ float s_w[kMaxSplits];
     __shared__ float s_red[kMergeThreads / kWave];
-    __shared__ float s_acc[2 * kDim + 4 * kMaxClusters];
+    __shared__ float4 s_d[8][kDim / 4];
+    __shared__ float4 s_b[16][kMaxClusters / 4];
     const long bq = blockIdx.x;  // b * Hq + hq
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int G = Hq / H;
@@ -562,33 +655,52 @@ __global__ void __launch_bounds__(kMergeThreads) decode_merge_kernel(
     __syncthreads();
     lsum = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
 
-    // 3) residual sums: thread = (channel, parity of the split index)
+    // 3) residual sums: thread = (split group tid / 32, channel quad tid % 32)
     {
-        const int c = tid & (kDim - 1), par = tid >> 7;
-        const float* base = pdelta + (bq * splits) * kDim + c;
-        float acc = 0.0f;
-#pragma unroll 4
-        for (int s = par; s < splits; s += 2) acc = fmaf(s_w[s], base[(long)s * kDim], acc);
-        s_acc[par * kDim + c] = acc;
+        const int grp = tid >> 5, cq = tid & 31;
+        const float4* base = reinterpret_cast<const float4*>(pdelta + (bq * splits) * kDim) + cq;
+        float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll 8
+        for (int s = grp; s < splits; s += 8) {
+            const float w = s_w[s];
+            const float4 d = base[(long)s * (kDim / 4)];
+            acc.x = fmaf(w, d.x, acc.x);
+            acc.y = fmaf(w, d.y, acc.y);
+            acc.z = fmaf(w, d.z, acc.z);
+            acc.w = fmaf(w, d.w, acc.w);
+        }
+        s_d[grp][cq] = acc;
     }
-    // 4) cluster mass: thread = (cluster, split index mod 4)
+    // 4) cluster mass: thread = (split group tid / 16, cluster quad tid % 16)
     {
-        const int c = tid & (kMaxClusters - 1), par = tid >> 6;
-        const float* base = pbeta + (bq * splits) * kMaxClusters + c;
-        float acc = 0.0f;
+        const int grp = tid >> 4, cq = tid & 15;
+        const float4* base = reinterpret_cast<const float4*>(pbeta + (bq * splits) * kMaxClusters) + cq;
+        float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll 4
-        for (int s = par; s < splits; s += 4) acc = fmaf(s_w[s], base[(long)s * kMaxClusters], acc);
-        s_acc[2 * kDim + par * kMaxClusters + c] = acc;
+        for (int s = grp; s < splits; s += 16) {
+            const float w = s_w[s];
+            const float4 d = base[(long)s * (kMaxClusters / 4)];
+            acc.x = fmaf(w, d.x, acc.x);
+            acc.y = fmaf(w, d.y, acc.y);
+            acc.z = fmaf(w, d.z, acc.z);
+            acc.w = fmaf(w, d.w, acc.w);
+        }
+        s_b[grp][cq] = acc;
     }
     __syncthreads();
     // 5) fold sum_c beta_c c_v[c], normalise (threads 0..127: one channel each)
     if (tid < kDim) {
-        float acc = s_acc[tid] + s_acc[kDim + tid];
+        const float* sd = reinterpret_cast<const float*>(s_d);
+        float acc = 0.0f;
+#pragma unroll
+        for (int g2 = 0; g2 < 8; ++g2) acc += sd[g2 * kDim + tid];
         if (vcent != nullptr) {
+            const float* sb = reinterpret_cast<const float*>(s_b);
             const uint16_t* vc = vcent + bh * vnc * kDim + tid;
-            const float* bb = s_acc + 2 * kDim;
             for (int c = 0; c < vnc; ++c) {
-                const float beta = (bb[c] + bb[kMaxClusters + c]) + (bb[2 * kMaxClusters + c] + bb[3 * kMaxClusters + c]);
+                float beta = 0.0f;
+#pragma unroll
+                for (int g2 = 0; g2 < 16; ++g2) beta += sb[g2 * kMaxClusters + c];
                 acc = fmaf(beta, h2f(vc[c * kDim]), acc);
             }
         }
@@ -646,10 +758,13 @@ __global__ void __launch_bounds__(64) merge_recent_kernel(
 // ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
+// Two 4-wave workgroups fit a CU at this kernel's register use, so about 512
+// workgroups fill the 256 CUs once; each wave keeps at least two 16-token
+// tiles so that its next tile's loads overlap the current tile's arithmetic.
 int auto_splits(int B, int H, int T) {
     const long heads = (long)B * H;
-    long s = (1024 + heads - 1) / heads;  // ~4 workgroups (16 waves) per CU over 256 CUs
-    const long cap = T / (kWaves * kTile) > 0 ? T / (kWaves * kTile) : 1;
+    long s = (512 + heads - 1) / heads;
+    const long cap = T / (kWaves * 2 * kTile) > 0 ? T / (kWaves * 2 * kTile) : 1;
     if (s > cap) s = cap;
     if (s > kMaxSplits) s = kMaxSplits;
     return (int)(s < 1 ? 1 : s);
@@ -669,8 +784,8 @@ int64_t workspace_for(int B, int Hq, int S) {
 
 int dfmt_of(const reskv_ctensor* c) {
     switch (c->format) {
-    case RESKV_FMT_BITMAP: return D_BITMAP;
-    case RESKV_FMT_TILED: return D_TILED;
+    case RESKV_FMT_BITMAP: return c->width > 64 ? D_BITMAP_W : D_BITMAP;
+    case RESKV_FMT_TILED: return c->width > 64 ? D_TILED_W : D_TILED;
     case RESKV_FMT_STRUCT16: return D_STRUCT16;
     case RESKV_FMT_STRUCT_INT4: return D_SINT4;
     default: return c->bits == 4 ? D_Q4 : D_Q2;
@@ -679,7 +794,7 @@ int dfmt_of(const reskv_ctensor* c) {
 
 int payload_bytes(int f, int width) {
     switch (f) {
-    case D_BITMAP: case D_TILED: case D_STRUCT16: return 2 * width;
+    case D_BITMAP: case D_TILED: case D_STRUCT16: case D_BITMAP_W: case D_TILED_W: return 2 * width;
     case D_SINT4: return 16;
     case D_Q4: return 64;
     case D_Q2: return 32;
@@ -733,6 +848,8 @@ int stage_bytes_rt(int f, int pb) {
     case D_SINT4: return stage_of<D_SINT4>(pb);
     case D_Q4: return stage_of<D_Q4>(pb);
     case D_Q2: return stage_of<D_Q2>(pb);
+    case D_BITMAP_W: return stage_of<D_BITMAP_W>(pb);
+    case D_TILED_W: return stage_of<D_TILED_W>(pb);
     default: return stage_of<D_DENSE>(pb);
     }
 }
@@ -762,6 +879,8 @@ int launch_partial(int kf, int vf, int G, dim3 grid, size_t shm, hipStream_t st,
         case D_SINT4: return launch_fmt<D_SINT4, D_SINT4>(G, grid, shm, st, p);
         case D_Q4: return launch_fmt<D_Q4, D_Q4>(G, grid, shm, st, p);
         case D_Q2: return launch_fmt<D_Q2, D_Q2>(G, grid, shm, st, p);
+        case D_BITMAP_W: return launch_fmt<D_BITMAP_W, D_BITMAP_W>(G, grid, shm, st, p);
+        case D_TILED_W: return launch_fmt<D_TILED_W, D_TILED_W>(G, grid, shm, st, p);
         default: return launch_fmt<D_DENSE, D_DENSE>(G, grid, shm, st, p);
         }
     }
@@ -799,9 +918,12 @@ int run_decode(const void* q, int kf, const DTensor& k, int vf, const DTensor& v
     const bool cent = kf != D_DENSE;
     const int merge_bytes = kWaves * G * kPartStride * 4;
     const int cent_bytes = cent ? k.nc * kDim * 4 : 0;
-    p.region0 = cent_bytes > merge_bytes ? cent_bytes : merge_bytes;
-    const int beta_bytes = cent ? kWaves * G * kMaxClusters * 4 : 0;
-    const size_t shm = (size_t)p.region0 + beta_bytes + (size_t)kWaves * (p.stage_k + p.stage_v);
+    const int region0 = cent_bytes > merge_bytes ? cent_bytes : merge_bytes;
+    p.beta_off = region0;
+    p.lut_off = p.beta_off + (cent ? kWaves * G * kMaxClusters * 4 : 0);
+    p.p_off = p.lut_off + kLutWords * 4;
+    p.stage_off = p.p_off + kWaves * kRows * kSteps * G * 4;
+    const size_t shm = (size_t)p.stage_off + (size_t)kWaves * (p.stage_k + p.stage_v);
     RESKV_REQUIRE(shm <= 65536, "decode LDS requirement %zu exceeds 64 KiB", shm);
     p.pm = (float*)ws;
     p.pl = p.pm + (long)B * Hq * S;
