@@ -44,6 +44,8 @@ def parse():
     p.add_argument("--no-sweep", action="store_true")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
+    p.add_argument("--only", choices=("encode", "quantized"), default=None,
+                   help="run just the config 1 (encode) or config 3 (quantized) measurement and print it")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="also run a 256 MiB device copy (reference point for HBM byte counters)")
     return p.parse_args()
@@ -354,6 +356,12 @@ def main():
         sys.exit(1)
     device = "cuda:0"
     torch.cuda.set_device(0)
+    if args.only == "encode":
+        print(json.dumps({"encode": measure_encoders(torch, device)}), flush=True)
+        return
+    if args.only == "quantized":
+        print(json.dumps({"quantized": measure_quantized(torch, device, max(5, args.steps // 2))}), flush=True)
+        return
     if args.calibrate_copy:
         src = torch.empty(256 << 20, dtype=torch.uint8, device=device).fill_(1)
         dst = torch.empty_like(src)
