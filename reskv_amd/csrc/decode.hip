@@ -43,6 +43,10 @@ constexpr int kMaxSplits = 1024;
 constexpr int kPartStride = kDim + kMaxClusters + 2;  // cross-wave merge record
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
+constexpr int kVPitch = kDim + 8;  // halves per token row of the V transpose tile (conflict-free writes)
+
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
 
 template <int F> struct Traits;
 template <> struct Traits<D_BITMAP> { static constexpr int MB = 16, PQ = 2; static constexpr bool SC = false, CENT = true; };
@@ -300,6 +304,72 @@ __device__ __forceinline__ void decode_res(const uint8_t* st, int tok, int pb, i
     }
 }
 
+// The same residuals as fp16 pairs for the matrix cores: h[0] = channels
+// (4i, 4i+1), h[1] = (4i+2, 4i+3), h[2], h[3] = the same of channels 64+4i...
+// FP16 formats hand their payload halves through unchanged; quantised codes
+// are dequantised in fp32 and rounded once to fp16.
+template <int F>
+__device__ __forceinline__ void decode_res_h(const uint8_t* st, int tok, int pb, int width, int li,
+                                             const uint32_t* lut, uint32_t* h) {
+    using Tr = Traits<F>;
+    const uint8_t* payb = st + tok * pb;
+    const uint8_t* meta = st + kTile * pb + tok * Tr::MB;
+    auto run = [&](int base, const uint32_t* tab, uint32_t v, uint32_t* out) {
+        const uint32_t* dw = reinterpret_cast<const uint32_t*>(payb) + (base >> 1);
+        const uint32_t d0 = dw[0], d1 = dw[1], d2 = dw[2];
+        const uint32_t sh = (uint32_t)(base & 1) * 16u;
+        const uint32_t w0 = __builtin_amdgcn_alignbit(d1, d0, sh);
+        const uint32_t w1 = __builtin_amdgcn_alignbit(d2, d1, sh);
+        const uint2 sel = *reinterpret_cast<const uint2*>(tab + 2 * v);
+        out[0] = __builtin_amdgcn_perm(w1, w0, sel.x);
+        out[1] = __builtin_amdgcn_perm(w1, w0, sel.y);
+    };
+    if constexpr (F == D_BITMAP || F == D_BITMAP_W) {
+        const uint4 m = *reinterpret_cast<const uint4*>(meta);
+        const uint64_t w0 = (uint64_t)m.x | ((uint64_t)m.y << 32);
+        const uint64_t w1 = (uint64_t)m.z | ((uint64_t)m.w << 32);
+        const int sh = 60 - 4 * li;
+        const uint32_t na = (uint32_t)(w0 >> sh) & 15u, nb = (uint32_t)(w1 >> sh) & 15u;
+        const int hi = 63 - 4 * li;
+        const int ba = li ? __builtin_popcountll((w0 >> 1) >> hi) : 0;
+        const int bb = __builtin_popcountll(w0) + (li ? __builtin_popcountll((w1 >> 1) >> hi) : 0);
+        run(ba, lut, na, h);
+        run(bb, lut, nb, h + 2);
+    } else if constexpr (F == D_TILED || F == D_TILED_W || F == D_STRUCT16) {
+        const uint4 m = *reinterpret_cast<const uint4*>(meta);
+        const uint32_t mw[4] = {m.x, m.y, m.z, m.w};
+        const int per_tile = F == D_STRUCT16 ? 4 : (width >> 3);
+        const int sub = li & 3;
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+            const int tile = (li >> 2) + 4 * half;
+            uint32_t code = (mw[tile >> 1] >> (16 * (tile & 1))) & 0xFFFFu;
+            if (F == D_STRUCT16) {
+                uint32_t mask = 0;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) mask |= 1u << ((code >> (4 * k)) & 15u);
+                code = mask;
+            }
+            const uint32_t nib = (code >> (4 * sub)) & 15u;
+            const int base = tile * per_tile + __builtin_popcount(code & ((1u << (4 * sub)) - 1u));
+            run(base, lut + 32, nib, h + 2 * half);
+        }
+    } else if constexpr (F == D_DENSE) {
+        const uint16_t* p16 = reinterpret_cast<const uint16_t*>(payb);
+        const uint2 a = *reinterpret_cast<const uint2*>(p16 + 4 * li);
+        const uint2 b = *reinterpret_cast<const uint2*>(p16 + 64 + 4 * li);
+        h[0] = a.x;
+        h[1] = a.y;
+        h[2] = b.x;
+        h[3] = b.y;
+    } else {
+        float r[8];
+        decode_res<F>(st, tok, pb, width, li, lut, r);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) h[k] = (uint32_t)f2h(r[2 * k]) | ((uint32_t)f2h(r[2 * k + 1]) << 16);
+    }
+}
+
 template <int F>
 __device__ __forceinline__ int stage_id(const uint8_t* st, int pb, int tok) {
     return reinterpret_cast<const int*>(st + kTile * pb + kTile * Traits<F>::MB)[tok];
@@ -363,7 +433,9 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
     float* s_cent = reinterpret_cast<float*>(smem);                          // region 0
     float* my_beta = reinterpret_cast<float*>(smem + P.beta_off) + wave * G * kMaxClusters;
     uint32_t* s_lut = reinterpret_cast<uint32_t*>(smem + P.lut_off);
-    float* my_p = reinterpret_cast<float*>(smem + P.p_off) + wave * kRows * NV;
+    // per wave: fp16 weights [step][head][row] and the V tile [token][kVPitch] for the matrix cores
+    uint16_t* my_p = reinterpret_cast<uint16_t*>(smem + P.p_off) + wave * (kSteps * G * kRows + kTile * kVPitch);
+    uint16_t* my_vt = my_p + kSteps * G * kRows;
     uint8_t* st_k = smem + P.stage_off + wave * (P.stage_k + P.stage_v);
     uint8_t* st_v = st_k + P.stage_k;
 
@@ -416,13 +488,15 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
         vg[k] = (v % NV) % G;
     }
 
-    float m[G], dl[G][8], lv[NVL];
+    // residual sums on the matrix cores (v_mfma_f32_4x4x4f16, 16 blocks of 4 lanes):
+    // lane L accumulates delta[4*gs + i][L + 64*half] in acc[gs][half][i]
+    constexpr int NGS = (G + 3) / 4;
+    float4_t acc[NGS][2];
+    float m[G], lv[NVL];
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-        m[g] = -INFINITY;
+    for (int gs = 0; gs < NGS; ++gs) acc[gs][0] = acc[gs][1] = (float4_t){0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int j = 0; j < 8; ++j) dl[g][j] = 0.0f;
-    }
+    for (int g = 0; g < G; ++g) m[g] = -INFINITY;
 #pragma unroll
     for (int k = 0; k < NVL; ++k) lv[k] = 0.0f;
     __syncthreads();
@@ -503,8 +577,8 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
 #pragma unroll
             for (int g = 0; g < G; ++g) {
                 const float alpha = exp2_fast(m[g] - mnew[g]);  // 0 on the first tile
-#pragma unroll
-                for (int j = 0; j < 8; ++j) dl[g][j] *= alpha;
+                acc[g >> 2][0][g & 3] *= alpha;
+                acc[g >> 2][1][g & 3] *= alpha;
                 if constexpr (KT::CENT) my_beta[g * kMaxClusters + lane] *= alpha;
 #pragma unroll
                 for (int k = 0; k < NVL; ++k) lv[k] = vg[k] == g ? lv[k] * alpha : lv[k];
@@ -520,10 +594,13 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
 #pragma unroll
                 for (int s = 0; s < kSteps; ++s) pick = (vs[k] == s && vg[k] == g) ? sc[g][s] : pick;
             }
-            const float pk_ = exp2_fast(pick - mg);
+            // the residual sums take the weight in fp16; the normaliser and the
+            // cluster mass use the same rounded weight so the average stays consistent
+            const uint16_t ph = f2h(exp2_fast(pick - mg));
+            const float pk_ = h2f(ph);
             if (vown[k]) {
                 lv[k] += pk_;
-                my_p[row * NV + li + 16 * k] = pk_;
+                my_p[(vs[k] * G + vg[k]) * kRows + row] = ph;
                 if constexpr (VT::CENT) {
                     const int vid = clamp_id(stage_id<VF>(st_v, P.v.pb, kRows * vs[k] + row), P.v.nc);
                     atomicAdd(&my_beta[vg[k] * kMaxClusters + vid], pk_);
@@ -532,19 +609,37 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
         }
         wave_sync();
 
-        // ---- values: residual sums ----
+        // ---- values: residuals as fp16 into the transpose tile, then P x V on the matrix cores ----
 #pragma unroll
         for (int s = 0; s < kSteps; ++s) {
             const int tok = kRows * s + row;
-            float vr[8];
-            decode_res<VF>(st_v, tok, P.v.pb, P.v.width, li, s_lut, vr);
-            float pg[G];
+            uint32_t hv[4];
+            decode_res_h<VF>(st_v, tok, P.v.pb, P.v.width, li, s_lut, hv);
+            *reinterpret_cast<uint2*>(my_vt + tok * kVPitch + 4 * li) = make_uint2(hv[0], hv[1]);
+            *reinterpret_cast<uint2*>(my_vt + tok * kVPitch + 64 + 4 * li) = make_uint2(hv[2], hv[3]);
+        }
+        wave_sync();
+        {
+            const int blk_row = lane & 3;  // A row (query head within the set) of this lane
 #pragma unroll
-            for (int g = 0; g < G; ++g) pg[g] = my_p[row * NV + s * G + g];
+            for (int s = 0; s < kSteps; ++s) {
+                // B: lane L holds V[tokens 4s + r, r = 0..3][channel L (+64)]
+                half4_t b0, b1;
 #pragma unroll
-            for (int g = 0; g < G; ++g)
+                for (int r = 0; r < 4; ++r) {
+                    b0[r] = __builtin_bit_cast(_Float16, my_vt[(kRows * s + r) * kVPitch + lane]);
+                    b1[r] = __builtin_bit_cast(_Float16, my_vt[(kRows * s + r) * kVPitch + 64 + lane]);
+                }
 #pragma unroll
-                for (int j = 0; j < 8; ++j) dl[g][j] = fmaf(pg[g], vr[j], dl[g][j]);
+                for (int gs = 0; gs < NGS; ++gs) {
+                    // A: lane 4b + i holds P[head 4*gs + i][tokens 4s + r]
+                    const int g = 4 * gs + blk_row;
+                    half4_t a = (half4_t){0, 0, 0, 0};
+                    if (g < G) a = __builtin_bit_cast(half4_t, *reinterpret_cast<const uint2*>(my_p + (s * G + g) * kRows));
+                    acc[gs][0] = __builtin_amdgcn_mfma_f32_4x4x4f16(a, b0, acc[gs][0], 0, 0, 0);
+                    acc[gs][1] = __builtin_amdgcn_mfma_f32_4x4x4f16(a, b1, acc[gs][1], 0, 0, 0);
+                }
+            }
         }
         wave_sync();  // stage and p reads done before the next tile overwrites them
     }
@@ -553,12 +648,10 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
     float lt[G];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-        float acc = 0.0f;
+        float ls = 0.0f;
 #pragma unroll
-        for (int k = 0; k < NVL; ++k) acc += (vown[k] && vg[k] == g) ? lv[k] : 0.0f;
-        lt[g] = wave_sum(acc);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) dl[g][j] = cross_rows_sum(dl[g][j]);
+        for (int k = 0; k < NVL; ++k) ls += (vown[k] && vg[k] == g) ? lv[k] : 0.0f;
+        lt[g] = wave_sum(ls);
     }
     float bt[G];
 #pragma unroll
@@ -568,13 +661,8 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
 #pragma unroll
     for (int g = 0; g < G; ++g) {
         float* e = rec + g * kPartStride;
-        if (row == 0) {
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                e[4 * li + j] = dl[g][j];
-                e[64 + 4 * li + j] = dl[g][4 + j];
-            }
-        }
+        e[lane] = acc[g >> 2][0][g & 3];
+        e[64 + lane] = acc[g >> 2][1][g & 3];
         e[kDim + lane] = bt[g];
         if (lane == 0) {
             e[kDim + kMaxClusters] = m[g];
@@ -856,6 +944,10 @@ int stage_bytes_rt(int f, int pb) {
 
 template <int G, int KF, int VF>
 int launch_g(dim3 grid, size_t shm, hipStream_t st, const DParams& p) {
+    if (shm > 65536 &&
+        hipFuncSetAttribute((const void*)decode_partial_kernel<G, KF, VF>,
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm) != hipSuccess)
+        return reskv_host::check_launch("decode LDS attribute");
     hipLaunchKernelGGL((decode_partial_kernel<G, KF, VF>), grid, dim3(kThreads), shm, st, p);
     return reskv_host::check_launch("decode_partial_kernel");
 }
@@ -922,9 +1014,9 @@ int run_decode(const void* q, int kf, const DTensor& k, int vf, const DTensor& v
     p.beta_off = region0;
     p.lut_off = p.beta_off + (cent ? kWaves * G * kMaxClusters * 4 : 0);
     p.p_off = p.lut_off + kLutWords * 4;
-    p.stage_off = p.p_off + kWaves * kRows * kSteps * G * 4;
+    p.stage_off = p.p_off + kWaves * (kSteps * G * kRows + kTile * kVPitch) * 2;
     const size_t shm = (size_t)p.stage_off + (size_t)kWaves * (p.stage_k + p.stage_v);
-    RESKV_REQUIRE(shm <= 65536, "decode LDS requirement %zu exceeds 64 KiB", shm);
+    RESKV_REQUIRE(shm <= 160 * 1024, "decode LDS requirement %zu exceeds 160 KiB", shm);
     p.pm = (float*)ws;
     p.pl = p.pm + (long)B * Hq * S;
     p.pd = p.pl + (long)B * Hq * S;
