@@ -30,7 +30,7 @@ extern "C" {
 /* Thread-local description of the last failure; "" when none. */
 const char* reskv_last_error(void);
 
-/* Library ABI version (bumped on any signature change). */
+/* Library ABI version (bumped on any signature or struct change); 2. */
 int reskv_abi_version(void);
 
 /* ------------------------------------------------------------------ *
@@ -104,7 +104,9 @@ enum reskv_format {
     RESKV_FMT_QUANT = 4        /* int32 payload [4*bits] signed codes + scale       */
 };
 
-/* One compressed tensor as the decode kernels read it. */
+/* One compressed tensor as the decode kernels read it.  Rows of (batch, head)
+ * bh start at bh * t_stride tokens (and bh * c_stride centroids), so a cache
+ * held in preallocated capacity buffers is read in place. */
 typedef struct reskv_ctensor {
     const void* centroids;   /* fp16 [B*H, nc, 128] */
     const int8_t* ids;       /* int8 [B*H, T] */
@@ -115,6 +117,10 @@ typedef struct reskv_ctensor {
     int format;              /* enum reskv_format */
     int width;               /* payload last-dim width (values or words) */
     int bits;                /* 16, 4 or 2 */
+    int t_stride;            /* tokens between consecutive (batch, head) rows of
+                                ids / payload / meta / scale; 0 means T (dense) */
+    int c_stride;            /* centroid rows between consecutive (batch, head)
+                                tables; 0 means nc (dense) */
 } reskv_ctensor;
 
 /* Bytes of split-K scratch reskv_decode needs; splits<=0 means automatic. */

@@ -43,13 +43,27 @@ def _stream(device):
     return torch.cuda.current_stream(device).cuda_stream
 
 
-def _dev_check(*tensors):
+def _dev_check(*tensors, contiguous=True):
     dev = tensors[0].device
     for t in tensors:
         if t is not None and t.numel() > 0:
             _require(t.is_cuda and t.device == dev, "all tensors must be on the same GPU")
-            _require(t.is_contiguous(), "tensors must be contiguous")
+            if contiguous:
+                _require(t.is_contiguous(), "tensors must be contiguous")
     return dev
+
+
+def _row_stride(t, width):
+    """Rows of a [BH, T(, width)] view: unit-stride within a token, token rows
+    `width` apart; returns the token stride between (batch, head) blocks."""
+    if t.dim() == 2:
+        _require(t.stride(1) == 1 or t.shape[1] == 1, "cache rows must be unit-stride")
+        return t.stride(0) if t.shape[0] > 1 else t.shape[1]
+    _require(t.stride(2) == 1 and (t.stride(1) == width or t.shape[1] == 1), "cache rows must be dense")
+    if t.shape[0] == 1:
+        return t.shape[1]
+    _require(t.stride(0) % width == 0, "cache blocks must start on a token row")
+    return t.stride(0) // width
 
 
 def _empty(shape, dtype, device):
@@ -186,24 +200,32 @@ def kmeans_assign(x, centers):
 # ---------------------------------------------------------------------------
 
 def _ctensor(cent, ids, payload, meta, scale, fmt, bits):
+    """Descriptor of one compressed tensor; the tensors may be views into
+    larger capacity buffers (rows of each (batch, head) block evenly strided)."""
     _require(cent.dtype == torch.float16 and cent.dim() == 3 and cent.shape[2] == 128,
              "centroids must be fp16 [B*nh_kv, nc, 128]")
     _require(ids.dtype == torch.int8 and ids.dim() == 2, "cluster ids must be int8 [B*nh_kv, T]")
     _require(payload.dim() == 3 and payload.shape[:2] == ids.shape, "payload must be [B*nh_kv, T, width]")
     _require(cent.shape[0] == ids.shape[0], "centroid batch-head mismatch")
+    ts = _row_stride(ids, 1)
+    _require(_row_stride(payload, payload.shape[2]) == ts, "payload and ids row strides differ")
     if meta is not None and meta.numel():
         _require(meta.dim() == 3 and meta.shape[:2] == ids.shape, "metadata shape mismatch")
+        _require(_row_stride(meta, meta.shape[2]) == ts, "metadata and ids row strides differ")
     if scale is not None and scale.numel():
         _require(scale.dtype == torch.float16 and tuple(scale.shape) == tuple(ids.shape), "scale shape mismatch")
+        _require(_row_stride(scale, 1) == ts, "scale and ids row strides differ")
+    cs = _row_stride(cent, 128)
     return _lib.CTensor(_ptr(cent), _ptr(ids), _ptr(payload), _ptr(meta), _ptr(scale), int(cent.shape[1]),
-                        int(fmt), int(payload.shape[2]), int(bits))
+                        int(fmt), int(payload.shape[2]), int(bits), int(ts), int(cs))
 
 
 def _decode(Q, kdesc, vdesc, keep, nh_kv, nh, start_pos, pos_q, rope_base, scaling, splits, inv_freq,
             return_stats=True):
     _require(Q.is_cuda and Q.dtype == torch.float16, "Q must be fp16 CUDA")
     _require(Q.dim() == 2 and Q.shape[1] == 128, "Q must be [B*nh, 128]")
-    _dev_check(Q, *keep)
+    _require(Q.is_contiguous(), "Q must be contiguous")
+    _dev_check(Q, *keep, contiguous=False)
     nh_kv, nh = int(nh_kv), int(nh)
     _require(nh % nh_kv == 0, "num_q_heads must be divisible by num_kv_heads")
     _require(nh // nh_kv in (1, 2, 4, 8), "supported GQA ratios are 1, 2, 4 and 8")

@@ -27,6 +27,8 @@ class CTensor(ctypes.Structure):
         ("format", _i),
         ("width", _i),
         ("bits", _i),
+        ("t_stride", _i),
+        ("c_stride", _i),
     ]
 
 

@@ -140,13 +140,20 @@ def compress(
             if bool(((ids < 0) | (ids >= centers.shape[2])).any()):
                 raise ValueError("external cluster IDs are out of range")
     elif previous is not None:
-        kc, ki = _incremental_cluster(key, previous.key.centroids, config)
-        vc, vi = _incremental_cluster(value, previous.value.centroids, config, value=True)
+        k, v = _compress_group(key, value, config, previous, plan)
+        return CompressedKV(previous.key.append(k), previous.value.append(v))
     else:
         kc, ki = cluster(key, config.num_clusters, config.kmeans_iterations)
         vc, vi = cluster(value, config.num_clusters, config.kmeans_iterations, value=True)
     k = _encode(key, kc, ki, plan)
     v = _encode(value, vc, vi, plan, value=True)
-    if previous is not None:
-        k, v = previous.key.append(k), previous.value.append(v)
     return CompressedKV(k, v)
+
+
+def _compress_group(key, value, config, previous, plan):
+    """One decode group against the shared centroid tables of ``previous``
+    (reskv/compression.py:160-169 without the final append): the group's own
+    compressed K and V, each carrying the extended centroid table."""
+    kc, ki = _incremental_cluster(key, previous.key.centroids, config)
+    vc, vi = _incremental_cluster(value, previous.value.centroids, config, value=True)
+    return _encode(key, kc, ki, plan), _encode(value, vc, vi, plan, value=True)

@@ -66,6 +66,7 @@ struct DTensor {
     const uint8_t* meta;      // [BH, T, MB bytes] or null
     const uint16_t* scale;    // fp16 [BH, T] or null
     int nc, width, pb;        // pb: payload bytes per token, a multiple of 16
+    int ts, cs;               // row strides: tokens per (batch, head) row block, centroid rows per table
 };
 
 struct DParams {
@@ -440,7 +441,7 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
     uint8_t* st_v = st_k + P.stage_k;
 
     if constexpr (KT::CENT) {
-        const uint16_t* kc = P.k.cent + bh * P.k.nc * kDim;
+        const uint16_t* kc = P.k.cent + bh * P.k.cs * kDim;
         for (int i = threadIdx.x; i < P.k.nc * kDim; i += kThreads) s_cent[i] = h2f(kc[i]);
 #pragma unroll
         for (int g = 0; g < G; ++g) my_beta[g * kMaxClusters + lane] = 0.0f;
@@ -506,8 +507,8 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
     Prefetch<VF> pv;
     if (ntiles > 0) {
         const int n = min(kTile, t1 - t0);
-        prefetch<KF>(P.k, bh * P.T + t0, n, lane, pk);
-        prefetch<VF>(P.v, bh * P.T + t0, n, lane, pv);
+        prefetch<KF>(P.k, bh * P.k.ts + t0, n, lane, pk);
+        prefetch<VF>(P.v, bh * P.v.ts + t0, n, lane, pv);
     }
     for (int tile = 0; tile < ntiles; ++tile) {
         const int tb = t0 + tile * kTile;
@@ -518,8 +519,8 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
         if (tile + 1 < ntiles) {
             const int tb2 = tb + kTile;
             const int n2 = min(kTile, t1 - tb2);
-            prefetch<KF>(P.k, bh * P.T + tb2, n2, lane, pk);
-            prefetch<VF>(P.v, bh * P.T + tb2, n2, lane, pv);
+            prefetch<KF>(P.k, bh * P.k.ts + tb2, n2, lane, pk);
+            prefetch<VF>(P.v, bh * P.v.ts + tb2, n2, lane, pv);
         }
         if ((tile & 7) == 0) rope_anchor(R, freq, (float)(P.start_pos + tb + row));
 
@@ -707,7 +708,7 @@ constexpr int kMergeThreads = 256;
 
 __global__ void __launch_bounds__(kMergeThreads) decode_merge_kernel(
     const float* __restrict__ pm, const float* __restrict__ pl, const float* __restrict__ pdelta,
-    const float* __restrict__ pbeta, const uint16_t* __restrict__ vcent, int vnc, int Hq, int H,
+    const float* __restrict__ pbeta, const uint16_t* __restrict__ vcent, int vnc, int vcs, int Hq, int H,
     int splits, uint16_t* __restrict__ out, float* __restrict__ om, float* __restrict__ ol) {
     __shared__ float s_w[kMaxSplits];
     __shared__ float s_red[kMergeThreads / kWave];
@@ -784,7 +785,7 @@ __global__ void __launch_bounds__(kMergeThreads) decode_merge_kernel(
         for (int g2 = 0; g2 < 8; ++g2) acc += sd[g2 * kDim + tid];
         if (vcent != nullptr) {
             const float* sb = reinterpret_cast<const float*>(s_b);
-            const uint16_t* vc = vcent + bh * vnc * kDim + tid;
+            const uint16_t* vc = vcent + bh * vcs * kDim + tid;
             for (int c = 0; c < vnc; ++c) {
                 float beta = 0.0f;
 #pragma unroll
@@ -920,9 +921,10 @@ int check_ct(const reskv_ctensor* c, const char* name) {
     return 0;
 }
 
-DTensor to_dt(const reskv_ctensor* c, int f) {
+DTensor to_dt(const reskv_ctensor* c, int f, int T) {
     return DTensor{(const uint16_t*)c->centroids, c->ids, (const uint8_t*)c->payload, (const uint8_t*)c->meta,
-                   (const uint16_t*)c->scale, c->nc, c->width, payload_bytes(f, c->width)};
+                   (const uint16_t*)c->scale, c->nc, c->width, payload_bytes(f, c->width),
+                   c->t_stride > 0 ? c->t_stride : T, c->c_stride > 0 ? c->c_stride : c->nc};
 }
 
 template <int F>
@@ -1024,7 +1026,7 @@ int run_decode(const void* q, int kf, const DTensor& k, int vf, const DTensor& v
     hipStream_t st = (hipStream_t)stream;
     if (launch_partial(kf, vf, G, dim3(S, H, B), shm, st, p)) return 1;
     hipLaunchKernelGGL(decode_merge_kernel, dim3(B * Hq), dim3(kMergeThreads), 0, st, p.pm, p.pl, p.pd, p.pb,
-                       cent ? v.cent : nullptr, v.nc, Hq, H, S, (uint16_t*)out, m, l);
+                       cent ? v.cent : nullptr, v.nc, v.cs, Hq, H, S, (uint16_t*)out, m, l);
     return reskv_host::check_launch("decode_merge_kernel");
 }
 
@@ -1046,9 +1048,13 @@ extern "C" int reskv_decode(const void* q, const reskv_ctensor* k, const reskv_c
                             int pos_q, float scaling, int splits, void* out, float* m, float* l,
                             void* workspace, int64_t workspace_bytes, void* stream) {
     if (check_ct(k, "K") || check_ct(v, "V")) return 1;
+    RESKV_REQUIRE((k->t_stride == 0 || k->t_stride >= T) && (v->t_stride == 0 || v->t_stride >= T),
+                  "token row stride must be 0 or at least T");
+    RESKV_REQUIRE((k->c_stride == 0 || k->c_stride >= k->nc) && (v->c_stride == 0 || v->c_stride >= v->nc),
+                  "centroid row stride must be 0 or at least nc");
     const int kf = dfmt_of(k), vf = dfmt_of(v);
-    return run_decode(q, kf, to_dt(k, kf), vf, to_dt(v, vf), inv_freq, B, Hq, H, T, start_pos, pos_q, scaling,
-                      splits, out, m, l, workspace, workspace_bytes, stream);
+    return run_decode(q, kf, to_dt(k, kf, T), vf, to_dt(v, vf, T), inv_freq, B, Hq, H, T, start_pos, pos_q,
+                      scaling, splits, out, m, l, workspace, workspace_bytes, stream);
 }
 
 extern "C" int reskv_decode_dense(const void* q, const void* k, const void* v, const float* inv_freq,
@@ -1057,8 +1063,8 @@ extern "C" int reskv_decode_dense(const void* q, const void* k, const void* v, c
                                   int64_t workspace_bytes, void* stream) {
     RESKV_REQUIRE(k && v, "null K/V pointer");
     RESKV_REQUIRE((((uintptr_t)k | (uintptr_t)v) & 15u) == 0, "K and V must be 16-byte aligned");
-    const DTensor kd{nullptr, nullptr, (const uint8_t*)k, nullptr, nullptr, 1, kDim, 2 * kDim};
-    const DTensor vd{nullptr, nullptr, (const uint8_t*)v, nullptr, nullptr, 1, kDim, 2 * kDim};
+    const DTensor kd{nullptr, nullptr, (const uint8_t*)k, nullptr, nullptr, 1, kDim, 2 * kDim, T, 1};
+    const DTensor vd{nullptr, nullptr, (const uint8_t*)v, nullptr, nullptr, 1, kDim, 2 * kDim, T, 1};
     return run_decode(q, D_DENSE, kd, D_DENSE, vd, inv_freq, B, Hq, H, T, start_pos, pos_q, scaling, splits, out,
                       m, l, workspace, workspace_bytes, stream);
 }

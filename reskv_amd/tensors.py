@@ -15,6 +15,13 @@ from .config import KernelPlan
 _ID_DTYPES = (torch.int8, torch.int16, torch.int32, torch.int64)
 
 
+def _rows(t: torch.Tensor) -> torch.Tensor:
+    """t when its innermost dimensions are dense (a [BH, T(, W)] block view), else a contiguous copy."""
+    inner_dense = t.stride(-1) == 1 and (t.dim() == 2 or t.stride(-2) == t.shape[-1] or t.shape[-2] == 1)
+    aligned = (t.storage_offset() * t.element_size()) % 16 == 0
+    return t if inner_dense and aligned else t.contiguous()
+
+
 def _check_metadata(plan: KernelPlan, metadata, shape3):
     spec = plan.metadata_spec
     if spec is None:
@@ -83,14 +90,17 @@ class CompressedTensor:
                 raise ValueError("quantized scales must be FP16 [B,H,T]")
         elif self.scale is not None:
             raise ValueError("FP16 sparse-only caches do not use quantization scales")
-        self.cluster_ids = ids.to(torch.int8).contiguous()
+        # int8 ids; tensors that are views into larger capacity buffers (rows of
+        # each (batch, head) block evenly strided) stay views: the kernels read
+        # them in place, and [B, H] merge into one dimension without a copy.
+        self.cluster_ids = ids if ids.dtype == torch.int8 else ids.to(torch.int8).contiguous()
         bh = b * h
         self._native = (
-            c.reshape(bh, -1, 128).contiguous(),
-            self.cluster_ids.view(bh, t),
-            p.reshape(bh, t, -1).contiguous(),
-            None if self.metadata is None else self.metadata.reshape(bh, t, -1).contiguous(),
-            None if self.scale is None else self.scale.reshape(bh, t).contiguous(),
+            _rows(c.reshape(bh, -1, 128)),
+            _rows(self.cluster_ids.reshape(bh, t)),
+            _rows(p.reshape(bh, t, -1)),
+            None if self.metadata is None else _rows(self.metadata.reshape(bh, t, -1)),
+            None if self.scale is None else _rows(self.scale.reshape(bh, t)),
         )
 
     @property

@@ -30,7 +30,7 @@ def test_library_exports_every_declared_symbol():
     for name in declared_functions():
         assert hasattr(lib, name), name
         assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
-    assert lib.reskv_abi_version() == 1
+    assert lib.reskv_abi_version() == 2
 
 
 def _err(status):

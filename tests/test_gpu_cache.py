@@ -1,0 +1,97 @@
+"""Device-resident two-segment cache with the real compressor (GPU).
+
+* The reference's incremental-cache invariants (reskv tests/test_cuda.py:74-89):
+  no token lost and centroid tables capped.
+* The capacity-buffer history equals, bit for bit, the chain the reference
+  builds with ``compress(..., previous=...)`` and ``torch.cat``.
+* Decode attention read in place from the capacity buffers (row-strided
+  views), joined with the dense ring, matches the float64 oracle.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import reskv_oracle as o
+from reskv_amd import ResKVKernelConfig, attention, compress
+from reskv_amd.cache import ResKVLayerCache
+from tests.gpu_helpers import ATOL, expected_attention, np_, seeded
+
+pytestmark = pytest.mark.gpu
+
+
+def _inputs(t, device, seed=4, b=1, h=2):
+    g = seeded(seed)
+    k = (torch.randn(b, h, t, 128, generator=g) * 0.5).half().to(device)
+    v = (torch.randn(b, h, t, 128, generator=g) * 0.5).half().to(device)
+    return k, v
+
+
+def test_incremental_cache_no_tokens_lost_and_centroids_capped(device):
+    cfg = ResKVKernelConfig(bits=16, layout="unstructured", num_clusters=4, max_clusters=6, group_size=16,
+                            recent_size=8)
+    cache = ResKVLayerCache(cfg)
+    k, v = _inputs(35, device)
+    cache.update(k, v, {"raw_keys": k})
+    assert cache.compressed.seq_len + cache.live == 35
+    for _ in range(100):
+        token = k[:, :, :1]
+        cache.update(token, token, {"raw_keys": token})
+        assert cache.compressed.seq_len + cache.live == cache.length
+        assert cache.compressed.key.centroids.shape[2] <= 6
+    assert cache.length == 135
+    cache.reset()
+    assert cache.get_seq_length() == 0 and cache.compressed is None
+
+
+@pytest.mark.parametrize("bits,sparsity", [(16, 0.5), (16, 0.75), (4, 0.5), (2, 0.5)])
+def test_capacity_history_equals_concatenated_chain(device, bits, sparsity):
+    cfg = ResKVKernelConfig(bits=bits, sparsity=sparsity, num_clusters=8, max_clusters=12, group_size=32,
+                            recent_size=16)
+    k, v = _inputs(200, device, seed=6)
+    layer = ResKVLayerCache(cfg, capacity=64)  # forces regrowth
+    layer.update(k[:, :, :100], v[:, :, :100], {"raw_keys": k[:, :, :100]})
+    for t in range(100, 200):
+        layer.update(k[:, :, t:t + 1], v[:, :, t:t + 1], {"raw_keys": k[:, :, t:t + 1]})
+    # the reference's chain: prefill compress, then one compress(previous=) per full ring
+    n0 = (100 - 16) // 32 * 32
+    ref = compress(k[:, :, :n0].contiguous(), v[:, :, :n0].contiguous(), cfg, plan=layer.plan)
+    done = n0
+    while done + 32 <= layer.compressed.seq_len:
+        ref = compress(k[:, :, done:done + 32].contiguous(), v[:, :, done:done + 32].contiguous(), cfg,
+                       previous=ref, plan=layer.plan)
+        done += 32
+    got = layer.compressed
+    assert got.seq_len == ref.seq_len == done
+    for a, b in ((got.key, ref.key), (got.value, ref.value)):
+        assert torch.equal(a.centroids, b.centroids)
+        assert torch.equal(a.cluster_ids, b.cluster_ids)
+        assert torch.equal(a.payload, b.payload)
+        assert (a.metadata is None) == (b.metadata is None)
+        if a.metadata is not None:
+            assert torch.equal(a.metadata, b.metadata)
+        if a.scale is not None:
+            assert torch.equal(a.scale, b.scale)
+
+
+@pytest.mark.parametrize("bits,sparsity", [(16, 0.5), (16, 0.75), (4, 0.5)])
+def test_decode_over_capacity_views_with_ring(device, bits, sparsity):
+    cfg = ResKVKernelConfig(bits=bits, sparsity=sparsity, num_clusters=8, max_clusters=16, group_size=32,
+                            recent_size=16)
+    b, h, gqa = 2, 2, 4
+    k, v = _inputs(260, device, seed=8, b=b, h=h)
+    freq = (500000.0 ** (-torch.arange(64, device=device).float() / 64)).float()
+    rot = lambda x, start: torch.from_numpy(  # noqa: E731
+        o.rotate(np_(x).astype(np.float64), np.arange(start, start + x.shape[2]), np_(freq))).half().to(device)
+    layer = ResKVLayerCache(cfg, capacity=96)
+    layer.update(rot(k[:, :, :180], 0), v[:, :, :180], {"raw_keys": k[:, :, :180]})
+    for t in range(180, 260):
+        layer.update(rot(k[:, :, t:t + 1], t), v[:, :, t:t + 1], {"raw_keys": k[:, :, t:t + 1]})
+    assert layer._k.ids.stride(1) > layer.compressed.seq_len  # a view with spare capacity
+    q = torch.randn(b, h * gqa, 1, 128, generator=seeded(9)).half().to(device)
+    pos = layer.length - 1
+    qr = rot(q, pos)
+    ring = (qr, layer.keys[:, :, : layer.live].contiguous(), layer.values[:, :, : layer.live].contiguous())
+    out = attention(q, layer.compressed, position=pos, inv_freq=freq, recent=ring)
+    ref = expected_attention(q, layer.compressed, position=pos, inv_freq=freq, recent=ring)
+    assert float(np.abs(np_(out).astype(np.float64) - ref).max()) <= ATOL
