@@ -143,6 +143,23 @@ int reskv_decode(const void* q, const reskv_ctensor* k, const reskv_ctensor* v,
                  int pos_q, float scaling, int splits, void* out, float* m, float* l,
                  void* workspace, int64_t workspace_bytes, void* stream);
 
+/* reskv_decode with a precomputed RoPE table (reskv_rope_table) covering
+ * positions [0, start_pos + T): per token the kernel reads cos/sin instead of
+ * evaluating them.  rope_table may be NULL (same as reskv_decode).  Replaces the
+ * same reference ops as reskv_decode; the table plays the part of the model's
+ * rotary cache (positions of compressed tokens never change, so one table
+ * serves every layer and decode step). */
+int reskv_decode_rope(const void* q, const reskv_ctensor* k, const reskv_ctensor* v,
+                      const float* inv_freq, const float* rope_table, int B, int Hq, int H, int T,
+                      int start_pos, int pos_q, float scaling, int splits, void* out, float* m,
+                      float* l, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* RoPE table for positions [0, count): fp32 [count][128], row p holding, for
+ * i0 = 0, 4, ..., 60, cos(fl32(p * inv_freq[i0 + j])) for j = 0..3 followed by
+ * the four sines.  Serves the same role as the rotary cos/sin cache that
+ * reskv/models/llama.py reads from the model (position_embeddings). */
+int reskv_rope_table(const float* inv_freq, int count, float* table, void* stream);
+
 /* Joint softmax of the compressed result with precomputed fp32 recent scores.
  * Replaces the deferred ext.merge_recent (reskv/csrc/cluster_mass.cu:1461-1508,
  * op at :1515).  comp_out fp16 [B*Hq,128]; comp_m, comp_l fp32 [B*Hq];

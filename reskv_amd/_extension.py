@@ -74,6 +74,29 @@ def _workspace(nbytes, device):
     return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
 
 
+# RoPE tables keyed by their frequencies: (device, data_ptr, version) of a
+# caller's inv_freq tensor, or (device, "theta", base).  Compressed tokens keep
+# their positions, so one table serves every layer and decode step.
+_ROPE_TABLES = {}
+_ROPE_TABLE_LIMIT = 16
+
+
+def _rope_table(freq, key, positions):
+    """fp32 [P, 128] table covering positions [0, positions), P a power of two."""
+    entry = _ROPE_TABLES.get(key)
+    if entry is not None and entry[0].shape[0] >= positions:
+        return entry[0]
+    count = 1 << max(10, (int(positions) - 1).bit_length())
+    table = torch.empty((count, 128), dtype=torch.float32, device=freq.device)
+    with torch.cuda.device(freq.device):
+        _lib.check(_lib.lib().reskv_rope_table(freq.data_ptr(), count, table.data_ptr(), _stream(freq.device)),
+                   "rope_table")
+    if len(_ROPE_TABLES) >= _ROPE_TABLE_LIMIT:
+        _ROPE_TABLES.pop(next(iter(_ROPE_TABLES)))
+    _ROPE_TABLES[key] = (table, freq)  # keeps the source tensor alive so its address is not reused
+    return table
+
+
 def _frequencies(inv_freq, rope_base, device):
     """The 64 RoPE frequencies: the caller's, or theta-derived (reskv/reference.py:73-77)."""
     if inv_freq is not None and inv_freq.numel():
@@ -237,15 +260,21 @@ def _decode(Q, kdesc, vdesc, keep, nh_kv, nh, start_pos, pos_q, rope_base, scali
     t = ids.shape[1]
     dev = Q.device
     freq = _frequencies(inv_freq, rope_base, dev)
+    if inv_freq is not None and inv_freq.numel():
+        key = (dev, inv_freq.data_ptr(), inv_freq._version)
+    else:
+        key = (dev, "theta", float(rope_base))
+    table = _rope_table(freq, key, int(start_pos) + t)
     L = _lib.lib()
     out = _empty((bnh, 128), torch.float16, dev)
     m = _empty((bnh,), torch.float32, dev)
     l = _empty((bnh,), torch.float32, dev)
     ws = _workspace(L.reskv_decode_workspace_bytes(b, nh, nh_kv, t, int(splits)), dev)
     with torch.cuda.device(dev):
-        _lib.check(L.reskv_decode(Q.data_ptr(), kdesc, vdesc, freq.data_ptr(), b, nh, nh_kv, t, int(start_pos),
-                                  int(pos_q), float(scaling), int(splits), out.data_ptr(), m.data_ptr(),
-                                  l.data_ptr(), ws.data_ptr(), ws.numel(), _stream(dev)), "decode")
+        _lib.check(L.reskv_decode_rope(Q.data_ptr(), kdesc, vdesc, freq.data_ptr(), table.data_ptr(), b, nh, nh_kv,
+                                       t, int(start_pos), int(pos_q), float(scaling), int(splits), out.data_ptr(),
+                                       m.data_ptr(), l.data_ptr(), ws.data_ptr(), ws.numel(), _stream(dev)),
+                   "decode")
     return [out, m, l] if return_stats else [out]
 
 

@@ -73,6 +73,7 @@ struct DParams {
     const uint16_t* q;
     DTensor k, v;
     const float* inv_freq;
+    const float4* rope;  // [position][16][cos x4, sin x4] table, or null (recurrence in-kernel)
     int Hq, H, T, start_pos, pos_q, splits;
     float qscale;  // scaling * log2(e): scores come out in the log2 domain
     int stage_k, stage_v;  // LDS stage bytes per wave for K and V
@@ -414,7 +415,7 @@ __device__ __forceinline__ void rope_anchor(Rope& R, const float* f, float pos) 
 // ---------------------------------------------------------------------------
 // partial kernel
 // ---------------------------------------------------------------------------
-template <int G, int KF, int VF>
+template <int G, int KF, int VF, bool TAB>
 __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
     extern __shared__ __align__(16) uint8_t smem[];
     using KT = Traits<KF>;
@@ -461,7 +462,7 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             rope_sincos_fast(__fmul_rn((float)P.pos_q, freq[j]), sn[j], cs[j]);
-            rope_sincos_fast(4.0f * freq[j], R.s4[j], R.c4[j]);  // 4f is exact in fp32
+            if (!TAB) rope_sincos_fast(4.0f * freq[j], R.s4[j], R.c4[j]);  // 4f is exact in fp32
         }
 #pragma unroll
         for (int g = 0; g < G; ++g) {
@@ -522,7 +523,17 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
             prefetch<KF>(P.k, bh * P.k.ts + tb2, n2, lane, pk);
             prefetch<VF>(P.v, bh * P.v.ts + tb2, n2, lane, pv);
         }
-        if ((tile & 7) == 0) rope_anchor(R, freq, (float)(P.start_pos + tb + row));
+        if (!TAB && (tile & 7) == 0) rope_anchor(R, freq, (float)(P.start_pos + tb + row));
+        // table rows of this lane's four steps: cos/sin of pairs 4i..4i+3 at the row's positions
+        float4 tc[kSteps], ts[kSteps];
+        if constexpr (TAB) {
+#pragma unroll
+            for (int s = 0; s < kSteps; ++s) {
+                const float4* tr = P.rope + ((long)(P.start_pos + tb + kRows * s + row) * 16 + li) * 2;
+                tc[s] = tr[0];
+                ts[s] = tr[1];
+            }
+        }
 
         // ---- scores of the tile's 16 tokens (log2 domain) ----
         float sc[G][kSteps];
@@ -540,17 +551,27 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
             }
             const float pos = (float)(P.start_pos + tb + tok);
             float xa[4], xb[4];
+            if constexpr (TAB) {
+                const float cs4[4] = {tc[s].x, tc[s].y, tc[s].z, tc[s].w};
+                const float sn4[4] = {ts[s].x, ts[s].y, ts[s].z, ts[s].w};
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const float hi = __fmul_rn(pos, freq[j]);
-                const float e = __builtin_fmaf(pos, freq[j], -hi);
-                const float cs = __builtin_fmaf(e, R.S[j], R.C[j]);
-                const float sn = __builtin_fmaf(-e, R.C[j], R.S[j]);
-                xa[j] = kr[j] * cs - kr[4 + j] * sn;
-                xb[j] = kr[4 + j] * cs + kr[j] * sn;
-                const float nc = R.C[j] * R.c4[j] - R.S[j] * R.s4[j];
-                R.S[j] = R.S[j] * R.c4[j] + R.C[j] * R.s4[j];
-                R.C[j] = nc;
+                for (int j = 0; j < 4; ++j) {
+                    xa[j] = kr[j] * cs4[j] - kr[4 + j] * sn4[j];
+                    xb[j] = kr[4 + j] * cs4[j] + kr[j] * sn4[j];
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float hi = __fmul_rn(pos, freq[j]);
+                    const float e = __builtin_fmaf(pos, freq[j], -hi);
+                    const float cs = __builtin_fmaf(e, R.S[j], R.C[j]);
+                    const float sn = __builtin_fmaf(-e, R.C[j], R.S[j]);
+                    xa[j] = kr[j] * cs - kr[4 + j] * sn;
+                    xb[j] = kr[4 + j] * cs + kr[j] * sn;
+                    const float nc = R.C[j] * R.c4[j] - R.S[j] * R.s4[j];
+                    R.S[j] = R.S[j] * R.c4[j] + R.C[j] * R.s4[j];
+                    R.C[j] = nc;
+                }
             }
             const bool valid = tok < n;
 #pragma unroll
@@ -944,14 +965,19 @@ int stage_bytes_rt(int f, int pb) {
     }
 }
 
-template <int G, int KF, int VF>
-int launch_g(dim3 grid, size_t shm, hipStream_t st, const DParams& p) {
+template <int G, int KF, int VF, bool TAB>
+int launch_gt(dim3 grid, size_t shm, hipStream_t st, const DParams& p) {
     if (shm > 65536 &&
-        hipFuncSetAttribute((const void*)decode_partial_kernel<G, KF, VF>,
+        hipFuncSetAttribute((const void*)decode_partial_kernel<G, KF, VF, TAB>,
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm) != hipSuccess)
         return reskv_host::check_launch("decode LDS attribute");
-    hipLaunchKernelGGL((decode_partial_kernel<G, KF, VF>), grid, dim3(kThreads), shm, st, p);
+    hipLaunchKernelGGL((decode_partial_kernel<G, KF, VF, TAB>), grid, dim3(kThreads), shm, st, p);
     return reskv_host::check_launch("decode_partial_kernel");
+}
+
+template <int G, int KF, int VF>
+int launch_g(dim3 grid, size_t shm, hipStream_t st, const DParams& p) {
+    return p.rope ? launch_gt<G, KF, VF, true>(grid, shm, st, p) : launch_gt<G, KF, VF, false>(grid, shm, st, p);
 }
 
 template <int KF, int VF>
@@ -984,9 +1010,9 @@ int launch_partial(int kf, int vf, int G, dim3 grid, size_t shm, hipStream_t st,
     return 1;
 }
 
-int run_decode(const void* q, int kf, const DTensor& k, int vf, const DTensor& v, const float* inv_freq, int B,
-               int Hq, int H, int T, int start_pos, int pos_q, float scaling, int splits, void* out, float* m,
-               float* l, void* ws, int64_t ws_bytes, void* stream) {
+int run_decode(const void* q, int kf, const DTensor& k, int vf, const DTensor& v, const float* inv_freq,
+               const float* rope, int B, int Hq, int H, int T, int start_pos, int pos_q, float scaling, int splits,
+               void* out, float* m, float* l, void* ws, int64_t ws_bytes, void* stream) {
     RESKV_REQUIRE(q && inv_freq && out, "null pointer argument");
     RESKV_REQUIRE(B > 0 && H > 0 && T > 0, "batch, head and token counts must be positive");
     RESKV_REQUIRE(Hq % H == 0, "query heads must be a multiple of KV heads");
@@ -1000,6 +1026,8 @@ int run_decode(const void* q, int kf, const DTensor& k, int vf, const DTensor& v
     p.k = k;
     p.v = v;
     p.inv_freq = inv_freq;
+    p.rope = (const float4*)rope;
+    RESKV_REQUIRE(((uintptr_t)rope & 15u) == 0, "RoPE table must be 16-byte aligned");
     p.Hq = Hq;
     p.H = H;
     p.T = T;
@@ -1043,18 +1071,26 @@ extern "C" int reskv_decode_splits(int B, int Hq, int H, int T, int splits) {
     return resolve_splits(B, H, T, splits);
 }
 
-extern "C" int reskv_decode(const void* q, const reskv_ctensor* k, const reskv_ctensor* v,
-                            const float* inv_freq, int B, int Hq, int H, int T, int start_pos,
-                            int pos_q, float scaling, int splits, void* out, float* m, float* l,
-                            void* workspace, int64_t workspace_bytes, void* stream) {
+extern "C" int reskv_decode_rope(const void* q, const reskv_ctensor* k, const reskv_ctensor* v,
+                                 const float* inv_freq, const float* rope_table, int B, int Hq, int H, int T,
+                                 int start_pos, int pos_q, float scaling, int splits, void* out, float* m,
+                                 float* l, void* workspace, int64_t workspace_bytes, void* stream) {
     if (check_ct(k, "K") || check_ct(v, "V")) return 1;
     RESKV_REQUIRE((k->t_stride == 0 || k->t_stride >= T) && (v->t_stride == 0 || v->t_stride >= T),
                   "token row stride must be 0 or at least T");
     RESKV_REQUIRE((k->c_stride == 0 || k->c_stride >= k->nc) && (v->c_stride == 0 || v->c_stride >= v->nc),
                   "centroid row stride must be 0 or at least nc");
     const int kf = dfmt_of(k), vf = dfmt_of(v);
-    return run_decode(q, kf, to_dt(k, kf, T), vf, to_dt(v, vf, T), inv_freq, B, Hq, H, T, start_pos, pos_q,
-                      scaling, splits, out, m, l, workspace, workspace_bytes, stream);
+    return run_decode(q, kf, to_dt(k, kf, T), vf, to_dt(v, vf, T), inv_freq, rope_table, B, Hq, H, T, start_pos,
+                      pos_q, scaling, splits, out, m, l, workspace, workspace_bytes, stream);
+}
+
+extern "C" int reskv_decode(const void* q, const reskv_ctensor* k, const reskv_ctensor* v,
+                            const float* inv_freq, int B, int Hq, int H, int T, int start_pos,
+                            int pos_q, float scaling, int splits, void* out, float* m, float* l,
+                            void* workspace, int64_t workspace_bytes, void* stream) {
+    return reskv_decode_rope(q, k, v, inv_freq, nullptr, B, Hq, H, T, start_pos, pos_q, scaling, splits, out, m, l,
+                             workspace, workspace_bytes, stream);
 }
 
 extern "C" int reskv_decode_dense(const void* q, const void* k, const void* v, const float* inv_freq,
@@ -1065,8 +1101,32 @@ extern "C" int reskv_decode_dense(const void* q, const void* k, const void* v, c
     RESKV_REQUIRE((((uintptr_t)k | (uintptr_t)v) & 15u) == 0, "K and V must be 16-byte aligned");
     const DTensor kd{nullptr, nullptr, (const uint8_t*)k, nullptr, nullptr, 1, kDim, 2 * kDim, T, 1};
     const DTensor vd{nullptr, nullptr, (const uint8_t*)v, nullptr, nullptr, 1, kDim, 2 * kDim, T, 1};
-    return run_decode(q, D_DENSE, kd, D_DENSE, vd, inv_freq, B, Hq, H, T, start_pos, pos_q, scaling, splits, out,
-                      m, l, workspace, workspace_bytes, stream);
+    return run_decode(q, D_DENSE, kd, D_DENSE, vd, inv_freq, nullptr, B, Hq, H, T, start_pos, pos_q, scaling,
+                      splits, out, m, l, workspace, workspace_bytes, stream);
+}
+
+// Table of cos/sin of the reference's RoPE angles fl32(p * inv_freq[i]) for
+// positions [0, count): row p holds, for each i0 = 4*li, cos of pairs i0..i0+3
+// then sin of the same pairs (512 bytes per position).
+__global__ void __launch_bounds__(256) rope_table_kernel(const float* __restrict__ inv_freq, int count,
+                                                         float* __restrict__ table) {
+    const long idx = (long)blockIdx.x * 256 + threadIdx.x;  // (position, pair)
+    if (idx >= (long)count * kHalf) return;
+    const int pos = (int)(idx / kHalf), pair = (int)(idx % kHalf);
+    float sn, cs;
+    rope_sincos_fast(__fmul_rn((float)pos, inv_freq[pair]), sn, cs);
+    float* row = table + (long)pos * kDim + (pair >> 2) * 8;
+    row[pair & 3] = cs;
+    row[4 + (pair & 3)] = sn;
+}
+
+extern "C" int reskv_rope_table(const float* inv_freq, int count, float* table, void* stream) {
+    RESKV_REQUIRE(inv_freq && table, "null pointer argument");
+    RESKV_REQUIRE(count > 0, "position count must be positive");
+    const long n = (long)count * kHalf;
+    hipLaunchKernelGGL(rope_table_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                       inv_freq, count, table);
+    return reskv_host::check_launch("rope_table_kernel");
 }
 
 extern "C" int reskv_merge_recent_scores(const void* comp_out, const float* comp_m, const float* comp_l,
