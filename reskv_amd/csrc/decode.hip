@@ -37,13 +37,12 @@ enum DFmt { D_BITMAP = 0, D_TILED, D_STRUCT16, D_SINT4, D_Q4, D_Q2, D_DENSE, D_B
 constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * kWave;
 constexpr int kTile = 16;      // tokens per wave tile
-constexpr int kRows = 4;       // tokens processed together (one per 16-lane row)
-constexpr int kSteps = kTile / kRows;
 constexpr int kMaxSplits = 1024;
 constexpr int kPartStride = kDim + kMaxClusters + 2;  // cross-wave merge record
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr int kVPitch = kDim + 8;  // halves per token row of the V transpose tile (conflict-free writes)
+constexpr int kCPitch = kDim + 8;  // halves per row of the LDS key-centroid table (staggered banks)
 
 typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
@@ -73,9 +72,10 @@ struct DParams {
     const uint16_t* q;
     DTensor k, v;
     const float* inv_freq;
-    const float4* rope;  // [position][16][cos x4, sin x4] table, or null (recurrence in-kernel)
+    const float4* rope;  // [position][16][cos x4, sin x4] table, or null (sin/cos evaluated in-kernel)
     int Hq, H, T, start_pos, pos_q, splits;
     float qscale;  // scaling * log2(e): scores come out in the log2 domain
+    float one;     // 1.0f, opaque to the compiler: fp16 + fp16 sums as one mixed-precision FMA
     int stage_k, stage_v;  // LDS stage bytes per wave for K and V
     int beta_off, lut_off, p_off, stage_off;  // LDS byte offsets (region 0 holds centroids / merge records)
     float* pm;
@@ -113,7 +113,8 @@ struct Prefetch {
     float sc;
 };
 
-// Loads the raw bytes of tokens [row0, row0 + n) of one tensor (row0 = bh*T + t).
+// Loads the raw bytes of tokens [row0, row0 + n) of one tensor (row0 = bh*T + t);
+// bytes past the n tokens are zero, so padded tokens decode to zero residuals.
 template <int F>
 __device__ __forceinline__ void prefetch(const DTensor& X, long row0, int n, int lane, Prefetch<F>& P) {
     using Tr = Traits<F>;
@@ -145,18 +146,34 @@ __device__ __forceinline__ void prefetch(const DTensor& X, long row0, int n, int
     }
 }
 
-// Stage layout (bytes): payload [16][pb] | meta [16][MB] | ids int32[16] | scale f32[16]
+// Stage layout (bytes): payload [16][pb + 16] | meta [16][MB] | ids int32[16] |
+// scale f32[16].  The 16-byte pad staggers consecutive payload rows over the
+// LDS banks (16 lanes read 16 different rows at similar offsets).
 template <int F>
-__device__ __forceinline__ void stage_store(const Prefetch<F>& P, uint8_t* st, int pb, int lane) {
-    using Tr = Traits<F>;
-    const int pieces = kTile * (pb >> 4);
-    uint4* pay = reinterpret_cast<uint4*>(st);
+__host__ __device__ constexpr int stage_bytes(int pb) {
+    return kTile * (pb + 16) + kTile * Traits<F>::MB + 2 * kTile * 4;
+}
+
+// LDS byte offsets of this lane's prefetch pieces inside the stage (piece
+// q = lane + 64 i is bytes [16 (q % per_tok), +16) of token row q / per_tok),
+// or -1 past the tile.  The same for every tile, so computed once.
+template <int F>
+__device__ __forceinline__ void stage_slots(int pb, int lane, int* slot) {
+    const int per_tok = pb >> 4;
 #pragma unroll
-    for (int i = 0; i < Tr::PQ; ++i) {
+    for (int i = 0; i < Traits<F>::PQ; ++i) {
         const int q = lane + kWave * i;
-        if (q < pieces) pay[q] = P.pay[i];
+        slot[i] = q < kTile * per_tok ? (q / per_tok) * (pb + 16) + (q % per_tok) * 16 : -1;
     }
-    uint8_t* meta = st + kTile * pb;
+}
+
+template <int F>
+__device__ __forceinline__ void stage_store(const Prefetch<F>& P, uint8_t* st, int pb, const int* slot, int lane) {
+    using Tr = Traits<F>;
+#pragma unroll
+    for (int i = 0; i < Tr::PQ; ++i)
+        if (slot[i] >= 0) *reinterpret_cast<uint4*>(st + slot[i]) = P.pay[i];
+    uint8_t* meta = st + kTile * (pb + 16);
     if (lane < kTile) {
         if constexpr (Tr::MB == 16) reinterpret_cast<uint4*>(meta)[lane] = P.meta;
         if constexpr (Tr::MB == 8) reinterpret_cast<uint2*>(meta)[lane] = make_uint2(P.meta.x, P.meta.y);
@@ -167,21 +184,33 @@ __device__ __forceinline__ void stage_store(const Prefetch<F>& P, uint8_t* st, i
 }
 
 template <int F>
-__host__ __device__ constexpr int stage_bytes(int pb) {
-    return kTile * pb + kTile * Traits<F>::MB + 2 * kTile * 4;
-}
+struct StageView {
+    const uint8_t* st;
+    int pp;  // payload row pitch (pb + 16)
+    __device__ const uint8_t* row(int t) const { return st + t * pp; }
+    __device__ const uint8_t* meta(int t) const { return st + kTile * pp + t * Traits<F>::MB; }
+    __device__ int id(int t) const {
+        return reinterpret_cast<const int*>(st + kTile * pp + kTile * Traits<F>::MB)[t];
+    }
+    __device__ float scale(int t) const {
+        return reinterpret_cast<const float*>(st + kTile * pp + kTile * Traits<F>::MB + kTile * 4)[t];
+    }
+};
 
 // ---------------------------------------------------------------------------
-// residual decoders (LDS stage -> 8 fp32 values of this lane's channels)
-// r[0..3] = channels 4i..4i+3, r[4..7] = channels 64+4i..64+4i+3
+// residual decoders.  Lane L = 16 g + t owns token t of the tile and channel
+// group g: channels 16g..16g+15 (values m = 0..15) and 64+16g..64+16g+15
+// (m = 16..31), i.e. the sixteen rotate-half RoPE pairs (m, m + 16).
+// FP16 formats yield the residuals as fp16 pairs h[i] = values (2i, 2i+1).
 //
-// FP16 formats: the kept values of a lane's 4-channel run are consecutive in
-// the payload row, starting at rank `base`.  The 8-byte window at `base` is
-// fetched with two dword reads plus an alignbit, and one v_perm per channel
-// pair scatters the window's halves onto the kept channels (zeros elsewhere).
-// The permute selectors depend only on the run's 4-bit keep pattern and come
-// from a 16-entry table in LDS (one table for MSB-first bitmaps, one for
-// LSB-first tile masks).
+// A group's channels are four runs of four.  The kept values of a run are
+// consecutive in the payload row, starting at rank `base`; the 8-byte window at
+// `base` is fetched with two dword reads plus an alignbit, and one v_perm per
+// channel pair scatters the window's halves onto the kept channels (zeros
+// elsewhere).  The permute selectors depend only on the run's 4-bit keep
+// pattern and come from a 16-entry table in LDS (one table for MSB-first
+// bitmaps, one for LSB-first tile masks).  The ranks of a lane's runs follow
+// from the first one by popcounts of the patterns.
 // ---------------------------------------------------------------------------
 constexpr int kLutWords = 64;  // [msb|lsb][pattern][lo|hi]
 
@@ -203,304 +232,344 @@ __host__ __device__ constexpr uint32_t perm_selector(uint32_t v, bool msb, int h
 
 __device__ __forceinline__ float half_lo(uint32_t w) { return h2f((uint16_t)(w & 0xFFFFu)); }
 __device__ __forceinline__ float half_hi(uint32_t w) { return h2f((uint16_t)(w >> 16)); }
+__device__ __forceinline__ int popc(uint32_t v) { return __builtin_popcount(v); }
+__device__ __forceinline__ int clamp_id(int id, int nc) { return id < 0 ? 0 : (id >= nc ? nc - 1 : id); }
 
-// Kept values of one 4-channel run, as fp32: window of the payload row at
-// rank `base`, scattered by the pattern's selectors.
-__device__ __forceinline__ void expand_run(const uint8_t* row, int base, const uint32_t* lut, uint32_t v,
-                                           float* r) {
+// Kept values of one 4-channel run as two fp16 pairs.
+__device__ __forceinline__ void run_h(const uint8_t* row, int base, const uint32_t* tab, uint32_t v, uint32_t* out) {
     const uint32_t* dw = reinterpret_cast<const uint32_t*>(row) + (base >> 1);
     const uint32_t d0 = dw[0], d1 = dw[1], d2 = dw[2];
     const uint32_t sh = (uint32_t)(base & 1) * 16u;
     const uint32_t w0 = __builtin_amdgcn_alignbit(d1, d0, sh);
     const uint32_t w1 = __builtin_amdgcn_alignbit(d2, d1, sh);
-    const uint2 sel = *reinterpret_cast<const uint2*>(lut + 2 * v);
-    const uint32_t lo = __builtin_amdgcn_perm(w1, w0, sel.x);
-    const uint32_t hi = __builtin_amdgcn_perm(w1, w0, sel.y);
-    r[0] = half_lo(lo);
-    r[1] = half_hi(lo);
-    r[2] = half_lo(hi);
-    r[3] = half_hi(hi);
+    const uint2 sel = *reinterpret_cast<const uint2*>(tab + 2 * v);
+    out[0] = __builtin_amdgcn_perm(w1, w0, sel.x);
+    out[1] = __builtin_amdgcn_perm(w1, w0, sel.y);
+}
+
+// Bits of a bitmap word's channels that come before group g (channel d sits at
+// bit 63 - d): bits [64 - 16 g, 63], split into the word's high and low dword.
+struct GroupMask {
+    uint32_t hi, lo;
+};
+__device__ __forceinline__ GroupMask group_mask(int g) {
+    return {g == 0 ? 0u : (g == 1 ? 0xFFFF0000u : 0xFFFFFFFFu), g == 3 ? 0xFFFF0000u : 0u};
 }
 
 template <int F>
-__device__ __forceinline__ void decode_res(const uint8_t* st, int tok, int pb, int width, int li,
-                                           const uint32_t* lut, float* r) {
-    using Tr = Traits<F>;
-    const uint8_t* payb = st + tok * pb;
-    const uint8_t* meta = st + kTile * pb + tok * Tr::MB;
+constexpr bool kHalfFmt = F == D_BITMAP || F == D_BITMAP_W || F == D_TILED || F == D_TILED_W ||
+                          F == D_STRUCT16 || F == D_DENSE;
+
+template <int F>
+__device__ __forceinline__ void residual_h(const StageView<F>& S, int t, int g, int width, GroupMask gm,
+                                           const uint32_t* lut, uint32_t* h) {
+    const uint8_t* row = S.row(t);
     if constexpr (F == D_BITMAP || F == D_BITMAP_W) {
-        // channel d <-> bit (63 - d % 64) of word d / 64; value index = rank (reference.py:22-26)
-        const uint4 m = *reinterpret_cast<const uint4*>(meta);
-        const uint64_t w0 = (uint64_t)m.x | ((uint64_t)m.y << 32);
-        const uint64_t w1 = (uint64_t)m.z | ((uint64_t)m.w << 32);
-        const int sh = 60 - 4 * li;
-        const uint32_t na = (uint32_t)(w0 >> sh) & 15u, nb = (uint32_t)(w1 >> sh) & 15u;
-        // bits above this lane's run: (w >> 1) >> (63 - 4i) keeps every shift below 64
-        const int hi = 63 - 4 * li;
-        const int ba = li ? __builtin_popcountll((w0 >> 1) >> hi) : 0;
-        const int bb = __builtin_popcountll(w0) + (li ? __builtin_popcountll((w1 >> 1) >> hi) : 0);
-        expand_run(payb, ba, lut, na, r);
-        expand_run(payb, bb, lut, nb, r + 4);
+        // words: channels 0..63 in (m.y:m.x), 64..127 in (m.w:m.z), MSB-first
+        // (reference.py:22-26); group g's 16 channels are the (g odd ? low : high)
+        // half of dword (g < 2 ? high : low), channel 16g + c at field bit 15 - c
+        const uint4 m = *reinterpret_cast<const uint4*>(S.meta(t));
+        const uint32_t sh = (g & 1) ? 0u : 16u;
+        const uint32_t f0 = ((g < 2 ? m.y : m.x) >> sh) & 0xFFFFu;
+        const uint32_t f1 = ((g < 2 ? m.w : m.z) >> sh) & 0xFFFFu;
+        int r0 = popc(m.y & gm.hi) + popc(m.x & gm.lo);
+        int r1 = popc(m.y) + popc(m.x) + popc(m.w & gm.hi) + popc(m.z & gm.lo);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const uint32_t a = (f0 >> (12 - 4 * u)) & 15u, c = (f1 >> (12 - 4 * u)) & 15u;
+            run_h(row, r0, lut, a, h + 2 * u);
+            run_h(row, r1, lut, c, h + 8 + 2 * u);
+            r0 += popc(a);
+            r1 += popc(c);
+        }
     } else if constexpr (F == D_TILED || F == D_TILED_W || F == D_STRUCT16) {
-        // word w = code(tile 2w) | code(tile 2w+1) << 16 (reference.py:36-47)
-        const uint4 m = *reinterpret_cast<const uint4*>(meta);
-        const uint32_t mw[4] = {m.x, m.y, m.z, m.w};
-        const int per_tile = F == D_STRUCT16 ? 4 : (width >> 3);
-        const int sub = li & 3;
+        // word w = code(tile 2w) | code(tile 2w+1) << 16 (reference.py:36-47);
+        // group g covers tiles g and 4 + g
+        const uint4 m = *reinterpret_cast<const uint4*>(S.meta(t));
+        const uint32_t sh = (uint32_t)(g & 1) * 16u;
+        uint32_t f0 = ((g < 2 ? m.x : m.y) >> sh) & 0xFFFFu;
+        uint32_t f1 = ((g < 2 ? m.z : m.w) >> sh) & 0xFFFFu;
+        if constexpr (F == D_STRUCT16) {
+            // four ascending in-tile channel indices -> 16-bit mask; the tile's
+            // four values are one 8-byte word, windows come from 64-bit shifts
+            uint32_t k0 = 0, k1 = 0;
 #pragma unroll
-        for (int half = 0; half < 2; ++half) {
-            const int tile = (li >> 2) + 4 * half;
-            uint32_t code = (mw[tile >> 1] >> (16 * (tile & 1))) & 0xFFFFu;
-            if (F == D_STRUCT16) {
-                // four ascending in-tile channel indices -> 16-bit mask
-                uint32_t mask = 0;
-#pragma unroll
-                for (int k = 0; k < 4; ++k) mask |= 1u << ((code >> (4 * k)) & 15u);
-                code = mask;
+            for (int j = 0; j < 4; ++j) {
+                k0 |= 1u << ((f0 >> (4 * j)) & 15u);
+                k1 |= 1u << ((f1 >> (4 * j)) & 15u);
             }
-            const uint32_t nib = (code >> (4 * sub)) & 15u;
-            const int base = tile * per_tile + __builtin_popcount(code & ((1u << (4 * sub)) - 1u));
-            expand_run(payb, base, lut + 32, nib, r + 4 * half);
-        }
-    } else if constexpr (F == D_SINT4) {
-        // 1 of 4 per subgroup: 2-bit position, signed nibble code, fp16 scale (reference.py:27-35)
-        const uint4 qp = *reinterpret_cast<const uint4*>(payb);
-        const uint2 qm = *reinterpret_cast<const uint2*>(meta);
-        const float s = reinterpret_cast<const float*>(st + kTile * pb + kTile * Tr::MB + kTile * 4)[tok];
-        const uint32_t qw[4] = {qp.x, qp.y, qp.z, qp.w};
+            const uint2 pa = reinterpret_cast<const uint2*>(row)[g];
+            const uint2 pb = reinterpret_cast<const uint2*>(row)[4 + g];
+            const uint64_t wa = (uint64_t)pa.x | ((uint64_t)pa.y << 32);
+            const uint64_t wb = (uint64_t)pb.x | ((uint64_t)pb.y << 32);
+            int r0 = 0, r1 = 0;
 #pragma unroll
-        for (int half = 0; half < 2; ++half) {
-            const int grp = li + 16 * half;
-            const uint32_t sel = ((half ? qm.y : qm.x) >> (2 * li)) & 3u;
-            const int code = (int)__builtin_amdgcn_sbfe((int)qw[grp >> 3], 4 * (grp & 7), 4);  // typed unsigned
-            const float val = (float)code * s;
+            for (int u = 0; u < 4; ++u) {
+                const uint32_t a = (k0 >> (4 * u)) & 15u, c = (k1 >> (4 * u)) & 15u;
+                const uint64_t xa = wa >> ((16 * r0) & 63), xb = wb >> ((16 * r1) & 63);
+                const uint2 sa = *reinterpret_cast<const uint2*>(lut + 32 + 2 * a);
+                const uint2 sb = *reinterpret_cast<const uint2*>(lut + 32 + 2 * c);
+                h[2 * u] = __builtin_amdgcn_perm((uint32_t)(xa >> 32), (uint32_t)xa, sa.x);
+                h[2 * u + 1] = __builtin_amdgcn_perm((uint32_t)(xa >> 32), (uint32_t)xa, sa.y);
+                h[8 + 2 * u] = __builtin_amdgcn_perm((uint32_t)(xb >> 32), (uint32_t)xb, sb.x);
+                h[8 + 2 * u + 1] = __builtin_amdgcn_perm((uint32_t)(xb >> 32), (uint32_t)xb, sb.y);
+                r0 += popc(a);
+                r1 += popc(c);
+            }
+        } else {
+            const int per_tile = width >> 3;
+            int r0 = g * per_tile, r1 = (4 + g) * per_tile;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) r[4 * half + j] = (uint32_t)j == sel ? val : 0.0f;
+            for (int u = 0; u < 4; ++u) {
+                const uint32_t a = (f0 >> (4 * u)) & 15u, c = (f1 >> (4 * u)) & 15u;
+                run_h(row, r0, lut + 32, a, h + 2 * u);
+                run_h(row, r1, lut + 32, c, h + 8 + 2 * u);
+                r0 += popc(a);
+                r1 += popc(c);
+            }
         }
-    } else if constexpr (F == D_Q4 || F == D_Q2) {
+    } else if constexpr (F == D_DENSE) {
+        const uint4* r = reinterpret_cast<const uint4*>(row);
+        const uint4 a = r[2 * g], b = r[2 * g + 1], c = r[8 + 2 * g], d = r[9 + 2 * g];
+        const uint32_t v[16] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w, c.x, c.y, c.z, c.w, d.x, d.y, d.z, d.w};
+#pragma unroll
+        for (int i = 0; i < 16; ++i) h[i] = v[i];
+    }
+}
+
+// Quantised residuals in fp32, value m of the lane's channels.
+template <int F>
+__device__ __forceinline__ void residual_f(const StageView<F>& S, int t, int g, float* r) {
+    const uint8_t* row = S.row(t);
+    const float s = S.scale(t);
+    if constexpr (F == D_Q4 || F == D_Q2) {
         // signed codes, channel d in word d / (32/bits) at bit (d % (32/bits)) * bits (reference.py:17-21)
         constexpr int bits = F == D_Q4 ? 4 : 2;
         constexpr int per_word = 32 / bits;
-        const uint32_t* qw = reinterpret_cast<const uint32_t*>(payb);
-        const float s = reinterpret_cast<const float*>(st + kTile * pb + kTile * 4)[tok];
+        const uint32_t* qw = reinterpret_cast<const uint32_t*>(row);
+        const int wl = (16 * g) / per_word, wh = (64 + 16 * g) / per_word;
 #pragma unroll
-        for (int half = 0; half < 2; ++half) {
-            const int d0 = 4 * li + 64 * half;
-            const int w = (int)qw[d0 / per_word];
-            const int off = (d0 % per_word) * bits;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) r[4 * half + j] = (float)(int)__builtin_amdgcn_sbfe(w, off + j * bits, bits) * s;
+        for (int m = 0; m < 16; ++m) {
+            const int lo = (int)qw[wl + m / per_word], hi = (int)qw[wh + m / per_word];
+            r[m] = (float)(int)__builtin_amdgcn_sbfe(lo, (m % per_word) * bits, bits) * s;
+            r[16 + m] = (float)(int)__builtin_amdgcn_sbfe(hi, (m % per_word) * bits, bits) * s;
         }
-    } else {  // dense fp16 rows
-        const uint16_t* p16 = reinterpret_cast<const uint16_t*>(payb);
-        const uint2 a = *reinterpret_cast<const uint2*>(p16 + 4 * li);
-        const uint2 b = *reinterpret_cast<const uint2*>(p16 + 64 + 4 * li);
-        r[0] = half_lo(a.x);
-        r[1] = half_hi(a.x);
-        r[2] = half_lo(a.y);
-        r[3] = half_hi(a.y);
-        r[4] = half_lo(b.x);
-        r[5] = half_hi(b.x);
-        r[6] = half_lo(b.y);
-        r[7] = half_hi(b.y);
+    } else if constexpr (F == D_SINT4) {
+        // 1 of 4 per subgroup of four channels: 2-bit position, signed nibble
+        // code, fp16 scale (reference.py:27-35); group g holds subgroups
+        // 4g..4g+3 and 16+4g..16+4g+3
+        const uint4 qp = *reinterpret_cast<const uint4*>(row);
+        const uint2 qm = *reinterpret_cast<const uint2*>(S.meta(t));
+        const uint32_t qw[4] = {qp.x, qp.y, qp.z, qp.w};
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int off = 4 * (4 * (g & 1) + u);
+            const float vl = (float)(int)__builtin_amdgcn_sbfe((int)qw[g >> 1], off, 4) * s;
+            const float vh = (float)(int)__builtin_amdgcn_sbfe((int)qw[2 + (g >> 1)], off, 4) * s;
+            const uint32_t sl = (qm.x >> (2 * (4 * g + u))) & 3u, shh = (qm.y >> (2 * (4 * g + u))) & 3u;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                r[4 * u + j] = (uint32_t)j == sl ? vl : 0.0f;
+                r[16 + 4 * u + j] = (uint32_t)j == shh ? vh : 0.0f;
+            }
+        }
     }
 }
 
-// The same residuals as fp16 pairs for the matrix cores: h[0] = channels
-// (4i, 4i+1), h[1] = (4i+2, 4i+3), h[2], h[3] = the same of channels 64+4i...
+// Key values of the lane's 32 channels (pre-RoPE, fp32): centroid + residual.
+// fp16 + fp16 (or fp16 + fp32) sums run as one mixed-precision FMA by `one`.
+template <int F>
+__device__ __forceinline__ void key_values(const StageView<F>& S, int t, int g, int width, GroupMask gm,
+                                           const uint32_t* lut, const uint16_t* s_cent, int nc, float one, float* x) {
+    uint32_t c[16];
+    if constexpr (Traits<F>::CENT) {
+        const int kid = clamp_id(S.id(t), nc);
+        const uint4* cr = reinterpret_cast<const uint4*>(s_cent + kid * kCPitch);
+        const uint4 a = cr[2 * g], b = cr[2 * g + 1], d = cr[8 + 2 * g], e = cr[9 + 2 * g];
+        const uint32_t v[16] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w, d.x, d.y, d.z, d.w, e.x, e.y, e.z, e.w};
+#pragma unroll
+        for (int i = 0; i < 16; ++i) c[i] = v[i];
+    }
+    if constexpr (kHalfFmt<F>) {
+        uint32_t h[16];
+        residual_h<F>(S, t, g, width, gm, lut, h);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            if constexpr (Traits<F>::CENT) {
+                x[2 * i] = __builtin_fmaf(half_lo(h[i]), one, half_lo(c[i]));
+                x[2 * i + 1] = __builtin_fmaf(half_hi(h[i]), one, half_hi(c[i]));
+            } else {
+                x[2 * i] = half_lo(h[i]);
+                x[2 * i + 1] = half_hi(h[i]);
+            }
+        }
+    } else {
+        float r[32];
+        residual_f<F>(S, t, g, r);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            x[2 * i] = __builtin_fmaf(half_lo(c[i]), one, r[2 * i]);
+            x[2 * i + 1] = __builtin_fmaf(half_hi(c[i]), one, r[2 * i + 1]);
+        }
+    }
+}
+
+// Value residuals of the lane's 32 channels as fp16 pairs for the matrix cores.
 // FP16 formats hand their payload halves through unchanged; quantised codes
 // are dequantised in fp32 and rounded once to fp16.
 template <int F>
-__device__ __forceinline__ void decode_res_h(const uint8_t* st, int tok, int pb, int width, int li,
+__device__ __forceinline__ void value_halves(const StageView<F>& S, int t, int g, int width, GroupMask gm,
                                              const uint32_t* lut, uint32_t* h) {
-    using Tr = Traits<F>;
-    const uint8_t* payb = st + tok * pb;
-    const uint8_t* meta = st + kTile * pb + tok * Tr::MB;
-    auto run = [&](int base, const uint32_t* tab, uint32_t v, uint32_t* out) {
-        const uint32_t* dw = reinterpret_cast<const uint32_t*>(payb) + (base >> 1);
-        const uint32_t d0 = dw[0], d1 = dw[1], d2 = dw[2];
-        const uint32_t sh = (uint32_t)(base & 1) * 16u;
-        const uint32_t w0 = __builtin_amdgcn_alignbit(d1, d0, sh);
-        const uint32_t w1 = __builtin_amdgcn_alignbit(d2, d1, sh);
-        const uint2 sel = *reinterpret_cast<const uint2*>(tab + 2 * v);
-        out[0] = __builtin_amdgcn_perm(w1, w0, sel.x);
-        out[1] = __builtin_amdgcn_perm(w1, w0, sel.y);
-    };
-    if constexpr (F == D_BITMAP || F == D_BITMAP_W) {
-        const uint4 m = *reinterpret_cast<const uint4*>(meta);
-        const uint64_t w0 = (uint64_t)m.x | ((uint64_t)m.y << 32);
-        const uint64_t w1 = (uint64_t)m.z | ((uint64_t)m.w << 32);
-        const int sh = 60 - 4 * li;
-        const uint32_t na = (uint32_t)(w0 >> sh) & 15u, nb = (uint32_t)(w1 >> sh) & 15u;
-        const int hi = 63 - 4 * li;
-        const int ba = li ? __builtin_popcountll((w0 >> 1) >> hi) : 0;
-        const int bb = __builtin_popcountll(w0) + (li ? __builtin_popcountll((w1 >> 1) >> hi) : 0);
-        run(ba, lut, na, h);
-        run(bb, lut, nb, h + 2);
-    } else if constexpr (F == D_TILED || F == D_TILED_W || F == D_STRUCT16) {
-        const uint4 m = *reinterpret_cast<const uint4*>(meta);
-        const uint32_t mw[4] = {m.x, m.y, m.z, m.w};
-        const int per_tile = F == D_STRUCT16 ? 4 : (width >> 3);
-        const int sub = li & 3;
-#pragma unroll
-        for (int half = 0; half < 2; ++half) {
-            const int tile = (li >> 2) + 4 * half;
-            uint32_t code = (mw[tile >> 1] >> (16 * (tile & 1))) & 0xFFFFu;
-            if (F == D_STRUCT16) {
-                uint32_t mask = 0;
-#pragma unroll
-                for (int k = 0; k < 4; ++k) mask |= 1u << ((code >> (4 * k)) & 15u);
-                code = mask;
-            }
-            const uint32_t nib = (code >> (4 * sub)) & 15u;
-            const int base = tile * per_tile + __builtin_popcount(code & ((1u << (4 * sub)) - 1u));
-            run(base, lut + 32, nib, h + 2 * half);
-        }
-    } else if constexpr (F == D_DENSE) {
-        const uint16_t* p16 = reinterpret_cast<const uint16_t*>(payb);
-        const uint2 a = *reinterpret_cast<const uint2*>(p16 + 4 * li);
-        const uint2 b = *reinterpret_cast<const uint2*>(p16 + 64 + 4 * li);
-        h[0] = a.x;
-        h[1] = a.y;
-        h[2] = b.x;
-        h[3] = b.y;
+    if constexpr (kHalfFmt<F>) {
+        residual_h<F>(S, t, g, width, gm, lut, h);
     } else {
-        float r[8];
-        decode_res<F>(st, tok, pb, width, li, lut, r);
+        float r[32];
+        residual_f<F>(S, t, g, r);
 #pragma unroll
-        for (int k = 0; k < 4; ++k) h[k] = (uint32_t)f2h(r[2 * k]) | ((uint32_t)f2h(r[2 * k + 1]) << 16);
+        for (int i = 0; i < 16; ++i) h[i] = (uint32_t)f2h(r[2 * i]) | ((uint32_t)f2h(r[2 * i + 1]) << 16);
     }
 }
 
-template <int F>
-__device__ __forceinline__ int stage_id(const uint8_t* st, int pb, int tok) {
-    return reinterpret_cast<const int*>(st + kTile * pb + kTile * Traits<F>::MB)[tok];
-}
-
-__device__ __forceinline__ int clamp_id(int id, int nc) { return id < 0 ? 0 : (id >= nc ? nc - 1 : id); }
-
-__device__ __forceinline__ float rows_max(float v) {
-    return fmaxf(fmaxf(readlane(v, 0), readlane(v, 16)), fmaxf(readlane(v, 32), readlane(v, 48)));
-}
-// sum over the four rows, result in every lane (lanes i, i+16, i+32, i+48)
-__device__ __forceinline__ float cross_rows_sum(float v) {
-    v += __shfl_xor(v, 16);
-    v += __shfl_xor(v, 32);
-    return v;
-}
-
 // ---------------------------------------------------------------------------
-// RoPE by recurrence.  A lane keeps (C, S) = cos/sin of the exact angle p*f of
-// its row's current position p (advanced by 4 positions per step with
-// precomputed cos/sin of 4f).  The angle the reference uses is hi = fl32(p*f);
-// e = p*f - hi is exact (one FMA), and cos(hi) = C + e*S, sin(hi) = S - e*C to
-// well below fp32 resolution (|e| <= ulp(hi)/2, so e^2 is negligible).
+// cross-lane reductions of the score layout
 // ---------------------------------------------------------------------------
-struct Rope {
-    float C[4], S[4], c4[4], s4[4];
-};
-
-__device__ __forceinline__ void rope_anchor(Rope& R, const float* f, float pos) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const float hi = __fmul_rn(pos, f[j]);
-        const float e = __builtin_fmaf(pos, f[j], -hi);
-        float sn, cs;
-        rope_sincos_fast(hi, sn, cs);
-        R.C[j] = __builtin_fmaf(-e, sn, cs);
-        R.S[j] = __builtin_fmaf(e, cs, sn);
-    }
+__device__ __forceinline__ float swap32_sum(float a, float b) {  // lanes < 32: a + a^32; others: b + b^32
+    const auto r = __builtin_amdgcn_permlane32_swap((uint32_t)f2i(a), (uint32_t)f2i(b), false, false);
+    return i2f((int)r[0]) + i2f((int)r[1]);
+}
+__device__ __forceinline__ float swap16_sum(float a, float b) {  // even rows: a + a^16; odd rows: b + b^16
+    const auto r = __builtin_amdgcn_permlane16_swap((uint32_t)f2i(a), (uint32_t)f2i(b), false, false);
+    return i2f((int)r[0]) + i2f((int)r[1]);
+}
+// Max / sum over the 16 lanes with the same (lane & 3), result in each of them.
+__device__ __forceinline__ float head_max(float v) {
+    v = fmaxf(v, dpp<0x124>(v));  // row_ror:4
+    v = fmaxf(v, dpp<0x128>(v));  // row_ror:8
+    auto a = __builtin_amdgcn_permlane32_swap((uint32_t)f2i(v), (uint32_t)f2i(v), false, false);
+    v = fmaxf(i2f((int)a[0]), i2f((int)a[1]));
+    auto c = __builtin_amdgcn_permlane16_swap((uint32_t)f2i(v), (uint32_t)f2i(v), false, false);
+    return fmaxf(i2f((int)c[0]), i2f((int)c[1]));
+}
+__device__ __forceinline__ float head_sum(float v) {
+    v += dpp<0x124>(v);
+    v += dpp<0x128>(v);
+    v = swap32_sum(v, v);
+    return swap16_sum(v, v);
 }
 
 // ---------------------------------------------------------------------------
 // partial kernel
+//
+// A wave walks 16-token tiles of its quarter of the split.  Lane L = 16 g + t
+// decodes token t, channel group g of K (centroid + residual, RoPE from the
+// table) and of V.  Scores run on v_mfma_f32_4x4x1f32: block b (lanes
+// 4b..4b+3) multiplies tokens 4(b&3)+i of group b>>2 by query heads j = 0..3
+// held in the same lanes, one channel per instruction, 32 instructions per
+// tile; two lane swaps then add the four groups, leaving lane L with the
+// score of token 4((L>>2)&3) + (L>>4) for head (L&3) (+4 for the second set
+// of four heads when G = 8).  The online softmax takes one exponential per
+// lane; the weights, rounded to fp16, drive P x V on v_mfma_f32_4x4x4f16
+// through a per-wave transpose tile, and the cluster mass beta accumulates
+// with LDS atomics.
 // ---------------------------------------------------------------------------
 template <int G, int KF, int VF, bool TAB>
 __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
     extern __shared__ __align__(16) uint8_t smem[];
     using KT = Traits<KF>;
     using VT = Traits<VF>;
-    constexpr int NV = kSteps * G;             // softmax values of one row per tile
-    constexpr int NVL = (NV + 15) / 16;        // values per lane
+    constexpr int NH = (G + 3) / 4;  // sets of four query heads
     const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
     const long bh = (long)b * P.H + h;
     const int s0 = (int)(((long)split * P.T) / P.splits);
     const int s1 = (int)(((long)(split + 1) * P.T) / P.splits);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int row = lane >> 4, li = lane & 15;
+    const int t = lane & 15, grp = lane >> 4;  // decode: token of the tile, channel group
+    const int hj = lane & 3;                     // query head of this lane within a set
+    const int stok = 4 * ((lane >> 2) & 3) + (lane >> 4);  // token of this lane's score
     // this wave's contiguous share of the split
     const int t0 = s0 + (int)(((long)wave * (s1 - s0)) / kWaves);
     const int t1 = s0 + (int)(((long)(wave + 1) * (s1 - s0)) / kWaves);
 
-    float* s_cent = reinterpret_cast<float*>(smem);                          // region 0
+    uint16_t* s_cent = reinterpret_cast<uint16_t*>(smem);  // region 0: fp16 key centroids [nc][kCPitch]
     float* my_beta = reinterpret_cast<float*>(smem + P.beta_off) + wave * G * kMaxClusters;
     uint32_t* s_lut = reinterpret_cast<uint32_t*>(smem + P.lut_off);
-    // per wave: fp16 weights [step][head][row] and the V tile [token][kVPitch] for the matrix cores
-    uint16_t* my_p = reinterpret_cast<uint16_t*>(smem + P.p_off) + wave * (kSteps * G * kRows + kTile * kVPitch);
-    uint16_t* my_vt = my_p + kSteps * G * kRows;
+    // per wave: fp16 weights [4-token group][head][token] and the V tile [token][kVPitch]
+    uint16_t* my_p = reinterpret_cast<uint16_t*>(smem + P.p_off) + wave * (kTile * G + kTile * kVPitch);
+    uint16_t* my_vt = my_p + kTile * G;
     uint8_t* st_k = smem + P.stage_off + wave * (P.stage_k + P.stage_v);
     uint8_t* st_v = st_k + P.stage_k;
+    const StageView<KF> SK{st_k, P.k.pb + 16};
+    const StageView<VF> SV{st_v, P.v.pb + 16};
+    const GroupMask gm = group_mask(grp);
 
     if constexpr (KT::CENT) {
-        const uint16_t* kc = P.k.cent + bh * P.k.cs * kDim;
-        for (int i = threadIdx.x; i < P.k.nc * kDim; i += kThreads) s_cent[i] = h2f(kc[i]);
+        const uint4* kc = reinterpret_cast<const uint4*>(P.k.cent + bh * P.k.cs * kDim);
+        for (int i = threadIdx.x; i < P.k.nc * (kDim / 8); i += kThreads)
+            *reinterpret_cast<uint4*>(s_cent + (i >> 4) * kCPitch + 8 * (i & 15)) = kc[i];
 #pragma unroll
         for (int g = 0; g < G; ++g) my_beta[g * kMaxClusters + lane] = 0.0f;
     }
     if (threadIdx.x < kLutWords) {
-        const uint32_t t = threadIdx.x;
-        s_lut[t] = perm_selector((t >> 1) & 15u, t < 32, (int)(t & 1));
+        const uint32_t i = threadIdx.x;
+        s_lut[i] = perm_selector((i >> 1) & 15u, i < 32, (int)(i & 1));
     }
 
-    // rotated, pre-scaled query: qa = channels 4i+j, qb = channels 64+4i+j
-    const float4 fq = *reinterpret_cast<const float4*>(P.inv_freq + 4 * li);
-    const float freq[4] = {fq.x, fq.y, fq.z, fq.w};
-    float qa[G][4], qb[G][4];
-    Rope R;
+    // rotated, pre-scaled query values of this lane's channels for heads 4 hs + hj
+    float fr[16];
     {
-        float sn[4], cs[4];
+        const float4* fq = reinterpret_cast<const float4*>(P.inv_freq + 16 * grp);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            rope_sincos_fast(__fmul_rn((float)P.pos_q, freq[j]), sn[j], cs[j]);
-            if (!TAB) rope_sincos_fast(4.0f * freq[j], R.s4[j], R.c4[j]);  // 4f is exact in fp32
+        for (int u = 0; u < 4; ++u) {
+            const float4 f = fq[u];
+            fr[4 * u] = f.x;
+            fr[4 * u + 1] = f.y;
+            fr[4 * u + 2] = f.z;
+            fr[4 * u + 3] = f.w;
         }
+    }
+    float qv[NH][32];
+    {
+        float sn[16], cs[16];
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
-            const uint16_t* qr = P.q + ((long)b * P.Hq + (long)h * G + g) * kDim;
-            const uint2 ua = *reinterpret_cast<const uint2*>(qr + 4 * li);
-            const uint2 ub = *reinterpret_cast<const uint2*>(qr + 64 + 4 * li);
-            const float a[4] = {half_lo(ua.x), half_hi(ua.x), half_lo(ua.y), half_hi(ua.y)};
-            const float c[4] = {half_lo(ub.x), half_hi(ub.x), half_lo(ub.y), half_hi(ub.y)};
+        for (int m = 0; m < 16; ++m) rope_sincos_fast(__fmul_rn((float)P.pos_q, fr[m]), sn[m], cs[m]);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                qa[g][j] = (a[j] * cs[j] - c[j] * sn[j]) * P.qscale;
-                qb[g][j] = (c[j] * cs[j] + a[j] * sn[j]) * P.qscale;
+        for (int hs = 0; hs < NH; ++hs) {
+            const int g = 4 * hs + hj;
+            uint32_t lo[8] = {0, 0, 0, 0, 0, 0, 0, 0}, hi[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+            if (g < G) {
+                const uint4* qr = reinterpret_cast<const uint4*>(P.q + ((long)b * P.Hq + (long)h * G + g) * kDim);
+                const uint4 a = qr[2 * grp], c = qr[2 * grp + 1], d = qr[8 + 2 * grp], e = qr[9 + 2 * grp];
+                const uint32_t vl[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
+                const uint32_t vh[8] = {d.x, d.y, d.z, d.w, e.x, e.y, e.z, e.w};
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    lo[i] = vl[i];
+                    hi[i] = vh[i];
+                }
+            }
+#pragma unroll
+            for (int m = 0; m < 16; ++m) {
+                const float a = (m & 1) ? half_hi(lo[m >> 1]) : half_lo(lo[m >> 1]);
+                const float c = (m & 1) ? half_hi(hi[m >> 1]) : half_lo(hi[m >> 1]);
+                qv[hs][m] = (a * cs[m] - c * sn[m]) * P.qscale;
+                qv[hs][16 + m] = (c * cs[m] + a * sn[m]) * P.qscale;
             }
         }
     }
 
-    // this lane's softmax values: v = li + 16k -> (step v / G, head v % G)
-    int vs[NVL], vg[NVL];
-    bool vown[NVL];
+    // P x V sums (v_mfma_f32_4x4x4f16, 16 blocks of 4 lanes): lane L
+    // accumulates delta[4 hs + i][L + 64 half] in acc[hs][half][i]
+    float4_t acc[NH][2];
+    float m_run[NH], lv[NH];
 #pragma unroll
-    for (int k = 0; k < NVL; ++k) {
-        const int v = li + 16 * k;
-        vown[k] = v < NV;
-        vs[k] = (v % NV) / G;
-        vg[k] = (v % NV) % G;
+    for (int hs = 0; hs < NH; ++hs) {
+        acc[hs][0] = acc[hs][1] = (float4_t){0.0f, 0.0f, 0.0f, 0.0f};
+        m_run[hs] = -INFINITY;
+        lv[hs] = 0.0f;
     }
-
-    // residual sums on the matrix cores (v_mfma_f32_4x4x4f16, 16 blocks of 4 lanes):
-    // lane L accumulates delta[4*gs + i][L + 64*half] in acc[gs][half][i]
-    constexpr int NGS = (G + 3) / 4;
-    float4_t acc[NGS][2];
-    float m[G], lv[NVL];
-#pragma unroll
-    for (int gs = 0; gs < NGS; ++gs) acc[gs][0] = acc[gs][1] = (float4_t){0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int g = 0; g < G; ++g) m[g] = -INFINITY;
-#pragma unroll
-    for (int k = 0; k < NVL; ++k) lv[k] = 0.0f;
+    int kslot[KT::PQ], vslot[VT::PQ];
+    stage_slots<KF>(P.k.pb, lane, kslot);
+    stage_slots<VF>(P.v.pb, lane, vslot);
     __syncthreads();
 
     const int ntiles = (t1 - t0 + kTile - 1) / kTile;
@@ -514,8 +583,8 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
     for (int tile = 0; tile < ntiles; ++tile) {
         const int tb = t0 + tile * kTile;
         const int n = min(kTile, t1 - tb);
-        stage_store<KF>(pk, st_k, P.k.pb, lane);
-        stage_store<VF>(pv, st_v, P.v.pb, lane);
+        stage_store<KF>(pk, st_k, P.k.pb, kslot, lane);
+        stage_store<VF>(pv, st_v, P.v.pb, vslot, lane);
         wave_sync();
         if (tile + 1 < ntiles) {
             const int tb2 = tb + kTile;
@@ -523,157 +592,146 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
             prefetch<KF>(P.k, bh * P.k.ts + tb2, n2, lane, pk);
             prefetch<VF>(P.v, bh * P.v.ts + tb2, n2, lane, pv);
         }
-        if (!TAB && (tile & 7) == 0) rope_anchor(R, freq, (float)(P.start_pos + tb + row));
-        // table rows of this lane's four steps: cos/sin of pairs 4i..4i+3 at the row's positions
-        float4 tc[kSteps], ts[kSteps];
+        // position of this lane's key token (padded tokens reuse the last one)
+        const int pos = P.start_pos + tb + min(t, n - 1);
+        float4 tr[8];
         if constexpr (TAB) {
+            const float4* trow = P.rope + (long)pos * (kDim / 4) + 8 * grp;
 #pragma unroll
-            for (int s = 0; s < kSteps; ++s) {
-                const float4* tr = P.rope + ((long)(P.start_pos + tb + kRows * s + row) * 16 + li) * 2;
-                tc[s] = tr[0];
-                ts[s] = tr[1];
-            }
+            for (int i = 0; i < 8; ++i) tr[i] = trow[i];
         }
 
-        // ---- scores of the tile's 16 tokens (log2 domain) ----
-        float sc[G][kSteps];
+        // ---- keys: centroid + residual, rotated ----
+        float x[32];
+        key_values<KF>(SK, t, grp, P.k.width, gm, s_lut, s_cent, P.k.nc, P.one, x);
 #pragma unroll
-        for (int s = 0; s < kSteps; ++s) {
-            const int tok = kRows * s + row;
-            float kr[8];
-            decode_res<KF>(st_k, tok, P.k.pb, P.k.width, li, s_lut, kr);
-            if constexpr (KT::CENT) {
-                const int kid = clamp_id(stage_id<KF>(st_k, P.k.pb, tok), P.k.nc);
-                const float4 ca = *reinterpret_cast<const float4*>(s_cent + kid * kDim + 4 * li);
-                const float4 cb = *reinterpret_cast<const float4*>(s_cent + kid * kDim + 64 + 4 * li);
-                kr[0] += ca.x; kr[1] += ca.y; kr[2] += ca.z; kr[3] += ca.w;
-                kr[4] += cb.x; kr[5] += cb.y; kr[6] += cb.z; kr[7] += cb.w;
-            }
-            const float pos = (float)(P.start_pos + tb + tok);
-            float xa[4], xb[4];
+        for (int u = 0; u < 4; ++u) {
+            float cs4[4], sn4[4];
             if constexpr (TAB) {
-                const float cs4[4] = {tc[s].x, tc[s].y, tc[s].z, tc[s].w};
-                const float sn4[4] = {ts[s].x, ts[s].y, ts[s].z, ts[s].w};
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    xa[j] = kr[j] * cs4[j] - kr[4 + j] * sn4[j];
-                    xb[j] = kr[4 + j] * cs4[j] + kr[j] * sn4[j];
-                }
+                cs4[0] = tr[2 * u].x; cs4[1] = tr[2 * u].y; cs4[2] = tr[2 * u].z; cs4[3] = tr[2 * u].w;
+                sn4[0] = tr[2 * u + 1].x; sn4[1] = tr[2 * u + 1].y; sn4[2] = tr[2 * u + 1].z; sn4[3] = tr[2 * u + 1].w;
             } else {
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const float hi = __fmul_rn(pos, freq[j]);
-                    const float e = __builtin_fmaf(pos, freq[j], -hi);
-                    const float cs = __builtin_fmaf(e, R.S[j], R.C[j]);
-                    const float sn = __builtin_fmaf(-e, R.C[j], R.S[j]);
-                    xa[j] = kr[j] * cs - kr[4 + j] * sn;
-                    xb[j] = kr[4 + j] * cs + kr[j] * sn;
-                    const float nc = R.C[j] * R.c4[j] - R.S[j] * R.s4[j];
-                    R.S[j] = R.S[j] * R.c4[j] + R.C[j] * R.s4[j];
-                    R.C[j] = nc;
-                }
+                for (int j = 0; j < 4; ++j) rope_sincos_fast(__fmul_rn((float)pos, fr[4 * u + j]), sn4[j], cs4[j]);
             }
-            const bool valid = tok < n;
 #pragma unroll
-            for (int g = 0; g < G; ++g) {
-                float part = 0.0f;
-#pragma unroll
-                for (int j = 0; j < 4; ++j) part = fmaf(qa[g][j], xa[j], fmaf(qb[g][j], xb[j], part));
-                const float score = row_sum16(part);
-                sc[g][s] = valid ? score : -INFINITY;
+            for (int j = 0; j < 4; ++j) {
+                const int mi = 4 * u + j;
+                const float lo = x[mi], hi = x[16 + mi];
+                x[mi] = lo * cs4[j] - hi * sn4[j];
+                x[16 + mi] = hi * cs4[j] + lo * sn4[j];
             }
         }
 
-        // ---- online softmax over the tile: one exponential per lane value ----
+        // ---- scores on the matrix cores, then the sum over the four groups ----
+        float sc[NH];
+#pragma unroll
+        for (int hs = 0; hs < NH; ++hs) {
+            float4_t sa = (float4_t){0.0f, 0.0f, 0.0f, 0.0f}, sb = sa;
+#pragma unroll
+            for (int mi = 0; mi < 32; mi += 2) {
+                sa = __builtin_amdgcn_mfma_f32_4x4x1f32(x[mi], qv[hs][mi], sa, 0, 0, 0);
+                sb = __builtin_amdgcn_mfma_f32_4x4x1f32(x[mi + 1], qv[hs][mi + 1], sb, 0, 0, 0);
+            }
+            const float u0 = swap32_sum(sa[0] + sb[0], sa[2] + sb[2]);
+            const float u1 = swap32_sum(sa[1] + sb[1], sa[3] + sb[3]);
+            sc[hs] = swap16_sum(u0, u1);
+        }
+
+        // ---- values: residuals as fp16 into the transpose tile ----
+        {
+            uint32_t hv[16];
+            value_halves<VF>(SV, t, grp, P.v.width, gm, s_lut, hv);
+            uint4* vr = reinterpret_cast<uint4*>(my_vt + t * kVPitch + 16 * grp);
+            vr[0] = make_uint4(hv[0], hv[1], hv[2], hv[3]);
+            vr[1] = make_uint4(hv[4], hv[5], hv[6], hv[7]);
+            vr[8] = make_uint4(hv[8], hv[9], hv[10], hv[11]);
+            vr[9] = make_uint4(hv[12], hv[13], hv[14], hv[15]);
+        }
+
+        // ---- online softmax over the tile: one exponential per lane ----
         bool grow = false;
-        float mnew[G];
+        float mnew[NH];
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
-            float mx = sc[g][0];
-#pragma unroll
-            for (int s = 1; s < kSteps; ++s) mx = fmaxf(mx, sc[g][s]);
-            mnew[g] = fmaxf(m[g], rows_max(mx));
-            grow |= mnew[g] > m[g];
+        for (int hs = 0; hs < NH; ++hs) {
+            const bool ok = stok < n && 4 * hs + hj < G;
+            sc[hs] = ok ? sc[hs] : -INFINITY;
+            mnew[hs] = fmaxf(m_run[hs], head_max(sc[hs]));
+            grow |= mnew[hs] > m_run[hs];
         }
-        if (grow) {
+        if (ballot(grow) != 0) {
 #pragma unroll
-            for (int g = 0; g < G; ++g) {
-                const float alpha = exp2_fast(m[g] - mnew[g]);  // 0 on the first tile
-                acc[g >> 2][0][g & 3] *= alpha;
-                acc[g >> 2][1][g & 3] *= alpha;
-                if constexpr (KT::CENT) my_beta[g * kMaxClusters + lane] *= alpha;
+            for (int hs = 0; hs < NH; ++hs) {
+                const float alpha = mnew[hs] > m_run[hs] ? exp2_fast(m_run[hs] - mnew[hs]) : 1.0f;
+                lv[hs] *= alpha;
+                m_run[hs] = mnew[hs];
+                // lanes 4q + i hold head i: every lane takes the four factors of its quad
+                const float al[4] = {dpp<0x00>(alpha), dpp<0x55>(alpha), dpp<0xAA>(alpha), dpp<0xFF>(alpha)};
 #pragma unroll
-                for (int k = 0; k < NVL; ++k) lv[k] = vg[k] == g ? lv[k] * alpha : lv[k];
-                m[g] = mnew[g];
+                for (int i = 0; i < 4; ++i) {
+                    acc[hs][0][i] *= al[i];
+                    acc[hs][1][i] *= al[i];
+                    if constexpr (VT::CENT) {
+                        if (4 * hs + i < G) my_beta[(4 * hs + i) * kMaxClusters + lane] *= al[i];
+                    }
+                }
             }
         }
+        const int vid = VT::CENT ? clamp_id(SV.id(stok), P.v.nc) : 0;
 #pragma unroll
-        for (int k = 0; k < NVL; ++k) {
-            float pick = sc[0][0], mg = m[0];
-#pragma unroll
-            for (int g = 0; g < G; ++g) {
-                mg = vg[k] == g ? m[g] : mg;
-#pragma unroll
-                for (int s = 0; s < kSteps; ++s) pick = (vs[k] == s && vg[k] == g) ? sc[g][s] : pick;
-            }
+        for (int hs = 0; hs < NH; ++hs) {
+            const int g = 4 * hs + hj;
+            const bool ok = stok < n && g < G;
             // the residual sums take the weight in fp16; the normaliser and the
             // cluster mass use the same rounded weight so the average stays consistent
-            const uint16_t ph = f2h(exp2_fast(pick - mg));
-            const float pk_ = h2f(ph);
-            if (vown[k]) {
-                lv[k] += pk_;
-                my_p[(vs[k] * G + vg[k]) * kRows + row] = ph;
-                if constexpr (VT::CENT) {
-                    const int vid = clamp_id(stage_id<VF>(st_v, P.v.pb, kRows * vs[k] + row), P.v.nc);
-                    atomicAdd(&my_beta[vg[k] * kMaxClusters + vid], pk_);
-                }
+            const uint16_t ph = f2h(ok ? exp2_fast(sc[hs] - m_run[hs]) : 0.0f);
+            const float pq = h2f(ph);
+            lv[hs] += pq;
+            if (g < G) my_p[((((lane >> 2) & 3) * G + g) << 2) + (lane >> 4)] = ph;
+            if constexpr (VT::CENT) {
+                if (ok) atomicAdd(&my_beta[g * kMaxClusters + vid], pq);
             }
         }
         wave_sync();
 
-        // ---- values: residuals as fp16 into the transpose tile, then P x V on the matrix cores ----
-#pragma unroll
-        for (int s = 0; s < kSteps; ++s) {
-            const int tok = kRows * s + row;
-            uint32_t hv[4];
-            decode_res_h<VF>(st_v, tok, P.v.pb, P.v.width, li, s_lut, hv);
-            *reinterpret_cast<uint2*>(my_vt + tok * kVPitch + 4 * li) = make_uint2(hv[0], hv[1]);
-            *reinterpret_cast<uint2*>(my_vt + tok * kVPitch + 64 + 4 * li) = make_uint2(hv[2], hv[3]);
-        }
-        wave_sync();
+        // ---- P x V on the matrix cores, four tokens per instruction ----
         {
             const int blk_row = lane & 3;  // A row (query head within the set) of this lane
 #pragma unroll
-            for (int s = 0; s < kSteps; ++s) {
+            for (int s = 0; s < kTile / 4; ++s) {
                 // B: lane L holds V[tokens 4s + r, r = 0..3][channel L (+64)]
                 half4_t b0, b1;
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    b0[r] = __builtin_bit_cast(_Float16, my_vt[(kRows * s + r) * kVPitch + lane]);
-                    b1[r] = __builtin_bit_cast(_Float16, my_vt[(kRows * s + r) * kVPitch + 64 + lane]);
+                    b0[r] = __builtin_bit_cast(_Float16, my_vt[(4 * s + r) * kVPitch + lane]);
+                    b1[r] = __builtin_bit_cast(_Float16, my_vt[(4 * s + r) * kVPitch + 64 + lane]);
                 }
 #pragma unroll
-                for (int gs = 0; gs < NGS; ++gs) {
-                    // A: lane 4b + i holds P[head 4*gs + i][tokens 4s + r]
-                    const int g = 4 * gs + blk_row;
+                for (int hs = 0; hs < NH; ++hs) {
+                    // A: lane 4b + i holds P[head 4 hs + i][tokens 4s + r]
+                    const int g = 4 * hs + blk_row;
                     half4_t a = (half4_t){0, 0, 0, 0};
-                    if (g < G) a = __builtin_bit_cast(half4_t, *reinterpret_cast<const uint2*>(my_p + (s * G + g) * kRows));
-                    acc[gs][0] = __builtin_amdgcn_mfma_f32_4x4x4f16(a, b0, acc[gs][0], 0, 0, 0);
-                    acc[gs][1] = __builtin_amdgcn_mfma_f32_4x4x4f16(a, b1, acc[gs][1], 0, 0, 0);
+                    if (g < G) a = __builtin_bit_cast(half4_t, *reinterpret_cast<const uint2*>(my_p + ((s * G + g) << 2)));
+                    acc[hs][0] = __builtin_amdgcn_mfma_f32_4x4x4f16(a, b0, acc[hs][0], 0, 0, 0);
+                    acc[hs][1] = __builtin_amdgcn_mfma_f32_4x4x4f16(a, b1, acc[hs][1], 0, 0, 0);
                 }
             }
         }
-        wave_sync();  // stage and p reads done before the next tile overwrites them
+        wave_sync();  // stage, tile and weight reads done before the next tile overwrites them
     }
 
-    // ---- fold the four rows, then merge the waves through LDS ----
-    float lt[G];
+    // ---- per-head totals, then merge the waves through LDS ----
+    float lt[G], mt[G];
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-        float ls = 0.0f;
+    for (int hs = 0; hs < NH; ++hs) {
+        const float ls = head_sum(lv[hs]);
 #pragma unroll
-        for (int k = 0; k < NVL; ++k) ls += (vown[k] && vg[k] == g) ? lv[k] : 0.0f;
-        lt[g] = wave_sum(ls);
+        for (int i = 0; i < 4; ++i) {
+            if (4 * hs + i < G) {
+                lt[4 * hs + i] = readlane(ls, i);
+                mt[4 * hs + i] = readlane(m_run[hs], i);
+            }
+        }
     }
     float bt[G];
 #pragma unroll
@@ -687,7 +745,7 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
         e[64 + lane] = acc[g >> 2][1][g & 3];
         e[kDim + lane] = bt[g];
         if (lane == 0) {
-            e[kDim + kMaxClusters] = m[g];
+            e[kDim + kMaxClusters] = mt[g];
             e[kDim + kMaxClusters + 1] = lt[g];
         }
     }
@@ -937,8 +995,9 @@ int check_ct(const reskv_ctensor* c, const char* name) {
     default:
         RESKV_REQUIRE(false, "%s: unknown residual format %d", name, c->format);
     }
-    const uintptr_t align = (uintptr_t)c->payload | (uintptr_t)(c->meta ? c->meta : c->payload);
-    RESKV_REQUIRE((align & 15u) == 0, "%s: payload and metadata must be 16-byte aligned", name);
+    const uintptr_t align = (uintptr_t)c->payload | (uintptr_t)(c->meta ? c->meta : c->payload) |
+                            (uintptr_t)(c->centroids ? c->centroids : c->payload);
+    RESKV_REQUIRE((align & 15u) == 0, "%s: payload, metadata and centroids must be 16-byte aligned", name);
     return 0;
 }
 
@@ -1020,7 +1079,7 @@ int run_decode(const void* q, int kf, const DTensor& k, int vf, const DTensor& v
     RESKV_REQUIRE(G == 1 || G == 2 || G == 4 || G == 8, "supported GQA ratios are 1, 2, 4 and 8");
     const int S = resolve_splits(B, H, T, splits);
     RESKV_REQUIRE(ws != nullptr && ws_bytes >= workspace_for(B, Hq, S), "decode workspace too small");
-    RESKV_REQUIRE(((uintptr_t)inv_freq & 15u) == 0, "inv_freq must be 16-byte aligned");
+    RESKV_REQUIRE((((uintptr_t)inv_freq | (uintptr_t)q) & 15u) == 0, "q and inv_freq must be 16-byte aligned");
     DParams p{};
     p.q = (const uint16_t*)q;
     p.k = k;
@@ -1035,16 +1094,17 @@ int run_decode(const void* q, int kf, const DTensor& k, int vf, const DTensor& v
     p.pos_q = pos_q;
     p.splits = S;
     p.qscale = scaling * kLog2e;
+    p.one = 1.0f;
     p.stage_k = stage_bytes_rt(kf, k.pb);
     p.stage_v = stage_bytes_rt(vf, v.pb);
     const bool cent = kf != D_DENSE;
     const int merge_bytes = kWaves * G * kPartStride * 4;
-    const int cent_bytes = cent ? k.nc * kDim * 4 : 0;
+    const int cent_bytes = cent ? k.nc * kCPitch * 2 : 0;
     const int region0 = cent_bytes > merge_bytes ? cent_bytes : merge_bytes;
     p.beta_off = region0;
     p.lut_off = p.beta_off + (cent ? kWaves * G * kMaxClusters * 4 : 0);
     p.p_off = p.lut_off + kLutWords * 4;
-    p.stage_off = p.p_off + kWaves * (kSteps * G * kRows + kTile * kVPitch) * 2;
+    p.stage_off = p.p_off + kWaves * (kTile * G + kTile * kVPitch) * 2;
     const size_t shm = (size_t)p.stage_off + (size_t)kWaves * (p.stage_k + p.stage_v);
     RESKV_REQUIRE(shm <= 160 * 1024, "decode LDS requirement %zu exceeds 160 KiB", shm);
     p.pm = (float*)ws;
