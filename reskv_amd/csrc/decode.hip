@@ -43,9 +43,12 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr int kVPitch = kDim + 8;  // halves per token row of the V transpose tile (conflict-free writes)
 constexpr int kCPitch = kDim + 8;  // halves per row of the LDS key-centroid table (staggered banks)
+constexpr int kBetaPitch = kMaxClusters + 1;  // cluster-mass row pitch: the heads of a token hit distinct banks
 
 typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef short short4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) short4_t lds_short4_t;
 
 template <int F> struct Traits;
 template <> struct Traits<D_BITMAP> { static constexpr int MB = 16, PQ = 2; static constexpr bool SC = false, CENT = true; };
@@ -235,10 +238,13 @@ __device__ __forceinline__ float half_hi(uint32_t w) { return h2f((uint16_t)(w >
 __device__ __forceinline__ int popc(uint32_t v) { return __builtin_popcount(v); }
 __device__ __forceinline__ int clamp_id(int id, int nc) { return id < 0 ? 0 : (id >= nc ? nc - 1 : id); }
 
-// Kept values of one 4-channel run as two fp16 pairs.
+// Kept values of one 4-channel run as two fp16 pairs.  The window needs a
+// third dword only for a full run (pattern 15) starting at an odd rank.
 __device__ __forceinline__ void run_h(const uint8_t* row, int base, const uint32_t* tab, uint32_t v, uint32_t* out) {
     const uint32_t* dw = reinterpret_cast<const uint32_t*>(row) + (base >> 1);
-    const uint32_t d0 = dw[0], d1 = dw[1], d2 = dw[2];
+    const uint32_t d0 = dw[0], d1 = dw[1];
+    uint32_t d2 = 0;
+    if ((base & 1) && v == 15u) d2 = dw[2];
     const uint32_t sh = (uint32_t)(base & 1) * 16u;
     const uint32_t w0 = __builtin_amdgcn_alignbit(d1, d0, sh);
     const uint32_t w1 = __builtin_amdgcn_alignbit(d2, d1, sh);
@@ -491,7 +497,7 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
     const int t1 = s0 + (int)(((long)(wave + 1) * (s1 - s0)) / kWaves);
 
     uint16_t* s_cent = reinterpret_cast<uint16_t*>(smem);  // region 0: fp16 key centroids [nc][kCPitch]
-    float* my_beta = reinterpret_cast<float*>(smem + P.beta_off) + wave * G * kMaxClusters;
+    float* my_beta = reinterpret_cast<float*>(smem + P.beta_off) + wave * G * kBetaPitch;
     uint32_t* s_lut = reinterpret_cast<uint32_t*>(smem + P.lut_off);
     // per wave: fp16 weights [4-token group][head][token] and the V tile [token][kVPitch]
     uint16_t* my_p = reinterpret_cast<uint16_t*>(smem + P.p_off) + wave * (kTile * G + kTile * kVPitch);
@@ -501,17 +507,17 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
     const StageView<KF> SK{st_k, P.k.pb + 16};
     const StageView<VF> SV{st_v, P.v.pb + 16};
     const GroupMask gm = group_mask(grp);
+    if (threadIdx.x < kLutWords) {
+        const uint32_t i = threadIdx.x;
+        s_lut[i] = perm_selector((i >> 1) & 15u, i < 32, (int)(i & 1));
+    }
 
     if constexpr (KT::CENT) {
         const uint4* kc = reinterpret_cast<const uint4*>(P.k.cent + bh * P.k.cs * kDim);
         for (int i = threadIdx.x; i < P.k.nc * (kDim / 8); i += kThreads)
             *reinterpret_cast<uint4*>(s_cent + (i >> 4) * kCPitch + 8 * (i & 15)) = kc[i];
 #pragma unroll
-        for (int g = 0; g < G; ++g) my_beta[g * kMaxClusters + lane] = 0.0f;
-    }
-    if (threadIdx.x < kLutWords) {
-        const uint32_t i = threadIdx.x;
-        s_lut[i] = perm_selector((i >> 1) & 15u, i < 32, (int)(i & 1));
+        for (int g = 0; g < G; ++g) my_beta[g * kBetaPitch + lane] = 0.0f;
     }
 
     // rotated, pre-scaled query values of this lane's channels for heads 4 hs + hj
@@ -672,7 +678,7 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
                     acc[hs][0][i] *= al[i];
                     acc[hs][1][i] *= al[i];
                     if constexpr (VT::CENT) {
-                        if (4 * hs + i < G) my_beta[(4 * hs + i) * kMaxClusters + lane] *= al[i];
+                        if (4 * hs + i < G) my_beta[(4 * hs + i) * kBetaPitch + lane] *= al[i];
                     }
                 }
             }
@@ -689,7 +695,7 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
             lv[hs] += pq;
             if (g < G) my_p[((((lane >> 2) & 3) * G + g) << 2) + (lane >> 4)] = ph;
             if constexpr (VT::CENT) {
-                if (ok) atomicAdd(&my_beta[g * kMaxClusters + vid], pq);
+                if (ok) atomicAdd(&my_beta[g * kBetaPitch + vid], pq);
             }
         }
         wave_sync();
@@ -697,15 +703,15 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
         // ---- P x V on the matrix cores, four tokens per instruction ----
         {
             const int blk_row = lane & 3;  // A row (query head within the set) of this lane
+            // B through transpose reads: lane i of 16-lane row R points at
+            // V[4s + i/4][16R + 4(i%4) ..+3] and receives V[4s + r][16R + i], r = 0..3
+            const uint16_t* vb = my_vt + ((lane & 15) >> 2) * kVPitch + 16 * (lane >> 4) + 4 * (lane & 3);
 #pragma unroll
             for (int s = 0; s < kTile / 4; ++s) {
-                // B: lane L holds V[tokens 4s + r, r = 0..3][channel L (+64)]
-                half4_t b0, b1;
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    b0[r] = __builtin_bit_cast(_Float16, my_vt[(4 * s + r) * kVPitch + lane]);
-                    b1[r] = __builtin_bit_cast(_Float16, my_vt[(4 * s + r) * kVPitch + 64 + lane]);
-                }
+                const half4_t b0 = __builtin_bit_cast(half4_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (lds_short4_t*)(vb + 4 * s * kVPitch)));
+                const half4_t b1 = __builtin_bit_cast(half4_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (lds_short4_t*)(vb + 4 * s * kVPitch + 64)));
 #pragma unroll
                 for (int hs = 0; hs < NH; ++hs) {
                     // A: lane 4b + i holds P[head 4 hs + i][tokens 4s + r]
@@ -735,7 +741,7 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
     }
     float bt[G];
 #pragma unroll
-    for (int g = 0; g < G; ++g) bt[g] = KT::CENT ? my_beta[g * kMaxClusters + lane] : 0.0f;
+    for (int g = 0; g < G; ++g) bt[g] = KT::CENT ? my_beta[g * kBetaPitch + lane] : 0.0f;
     __syncthreads();  // centroid table and stages no longer needed
     float* rec = reinterpret_cast<float*>(smem) + wave * G * kPartStride;
 #pragma unroll
@@ -1102,7 +1108,7 @@ int run_decode(const void* q, int kf, const DTensor& k, int vf, const DTensor& v
     const int cent_bytes = cent ? k.nc * kCPitch * 2 : 0;
     const int region0 = cent_bytes > merge_bytes ? cent_bytes : merge_bytes;
     p.beta_off = region0;
-    p.lut_off = p.beta_off + (cent ? kWaves * G * kMaxClusters * 4 : 0);
+    p.lut_off = p.beta_off + (cent ? (kWaves * G * kBetaPitch * 4 + 15) / 16 * 16 : 0);
     p.p_off = p.lut_off + kLutWords * 4;
     p.stage_off = p.p_off + kWaves * (kTile * G + kTile * kVPitch) * 2;
     const size_t shm = (size_t)p.stage_off + (size_t)kWaves * (p.stage_k + p.stage_v);
