@@ -44,7 +44,10 @@ def parse():
     p.add_argument("--no-sweep", action="store_true")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
-    p.add_argument("--only", choices=("encode", "quantized"), default=None,
+    p.add_argument("--e2e-steps", type=int, default=2048, help="new tokens per sequence for --only e2e")
+    p.add_argument("--e2e-batch", type=int, default=16)
+    p.add_argument("--e2e-prompt", type=int, default=8192)
+    p.add_argument("--only", choices=("encode", "quantized", "e2e"), default=None,
                    help="run just the config 1 (encode) or config 3 (quantized) measurement and print it")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="also run a 256 MiB device copy (reference point for HBM byte counters)")
@@ -284,6 +287,72 @@ def measure_point_bits(torch, b, t, bits, layers, steps, device):
             "frac": nbytes / per_call / HBM_PEAK, "splits": nsplit}
 
 
+def measure_e2e(torch, device, batch=16, prompt=8192, steps=2048, warmup=4, attn_steps=8):
+    """Config 4: greedy decode of a random-init Llama-3.1-8B-shaped model (32 layers,
+    hidden 4096, 32/8 heads, FFN 14336, vocab 128256, llama3 RoPE theta 500000) at
+    batch 16 after an 8192-token random prompt, with the ResKV cache (75%, 32
+    clusters, 10 iterations, window 32, group 64) and with dense fp16 KV.  Reports
+    decode tok/s, TPOT and the attention share of the step time."""
+    from reskv_amd import ResKVKernelConfig
+    from reskv_amd.llama import GreedyDecoder, LlamaShape, RandomLlama
+
+    shape = LlamaShape()
+    model = RandomLlama(shape, device, seed=0)
+    ids = torch.randint(128, shape.vocab, (batch, prompt), generator=torch.Generator().manual_seed(42)).to(device)
+    cfg = ResKVKernelConfig(sparsity=0.75, num_clusters=32, kmeans_iterations=10, recent_size=32, group_size=64)
+    total = warmup + steps + attn_steps
+    decs = {"reskv": GreedyDecoder(model, batch, prompt, total, "reskv", cfg),
+            "dense_fp16": GreedyDecoder(model, batch, prompt, total, "dense")}
+
+    def sink(layer, raw_k, rot_k, v):
+        for d in decs.values():
+            d.absorb(layer, raw_k, rot_k, v)
+
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    first = model.prefill(ids, sink)
+    torch.cuda.synchronize()
+    out = {"prefill_s_incl_compression": time.perf_counter() - t0, "batch": batch, "prompt": prompt,
+           "new_tokens": steps, "model": "random-init Llama-3.1-8B shape (fp16 weights)"}
+    for name, dec in decs.items():
+        dec.start(first)
+        dec.capture()
+        for _ in range(warmup):
+            dec.step()
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        for _ in range(steps):
+            dec.step()
+        torch.cuda.synchronize()
+        secs = time.perf_counter() - t1
+        events = []
+        s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s0.record()
+        for _ in range(attn_steps):
+            dec.step(events)
+        s1.record()
+        torch.cuda.synchronize()
+        step_ms = s0.elapsed_time(s1) / attn_steps
+        attn_ms = sum(a.elapsed_time(b) for a, b in events) / attn_steps
+        out[name] = {"tok_per_s": batch * steps / secs, "tpot_ms": secs / steps * 1e3,
+                     "attention_ms_per_step": attn_ms, "step_ms_timed_with_events": step_ms,
+                     "attention_share": attn_ms / step_ms}
+        if name == "reskv":
+            out[name]["cache_mb_per_layer"] = _reskv_cache_mb(dec)
+    out["speedup_tok_per_s"] = out["reskv"]["tok_per_s"] / out["dense_fp16"]["tok_per_s"]
+    return out
+
+
+def _reskv_cache_mb(dec):
+    layer = dec.caches[0]
+    c = layer.compressed
+    n = sum(x.numel() * x.element_size() for t in (c.key, c.value)
+            for x in (t.centroids, t.cluster_ids, t.payload, t.metadata, t.scale) if x is not None)
+    ring = 3 * layer.keys.numel() * layer.keys.element_size()
+    return {"compressed": n / 1e6, "ring": ring / 1e6,
+            "dense_fp16_same_length": 2 * dec.batch * 8 * layer.length * 128 * 2 / 1e6}
+
+
 def cpu_baseline(seconds_budget, t, sparsity):
     """numpy oracle decode (reconstruct + float64 attention) on one batch element."""
     import numpy as np
@@ -361,6 +430,10 @@ def main():
         return
     if args.only == "quantized":
         print(json.dumps({"quantized": measure_quantized(torch, device, max(5, args.steps // 2))}), flush=True)
+        return
+    if args.only == "e2e":
+        print(json.dumps({"e2e": measure_e2e(torch, device, args.e2e_batch, args.e2e_prompt, args.e2e_steps)}),
+              flush=True)
         return
     if args.calibrate_copy:
         src = torch.empty(256 << 20, dtype=torch.uint8, device=device).fill_(1)

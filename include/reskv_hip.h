@@ -170,19 +170,23 @@ int reskv_merge_recent_scores(const void* comp_out, const float* comp_m, const f
 
 /* Joint softmax of the compressed result with dense rotated recent tokens.
  * Replaces the per-token ext.merge_recent (reskv/csrc/attention.cu:839-906,
- * op at :1355).  q_rope fp16 [B*Hq,128]; k_recent, v_recent fp16 [B,H,Tr,128]. */
+ * op at :1355).  q_rope fp16 [B*Hq,128]; k_recent, v_recent fp16 [B,H,*,128]:
+ * the first Tr tokens of rows of r_stride tokens (r_stride<=0: Tr), so that a
+ * ring buffer is read in place. */
 int reskv_merge_recent_qk(const void* comp_out, const float* comp_m, const float* comp_l,
                           const void* q_rope, const void* k_recent, const void* v_recent,
-                          int B, int Hq, int H, int Tr, float scaling, void* out,
+                          int B, int Hq, int H, int Tr, int r_stride, float scaling, void* out,
                           void* stream);
 
 /* Dense fp16 decode attention (the uncompressed baseline at the same shapes):
- * q fp16 [B*Hq,128] pre-RoPE, k fp16 [B,H,T,128] pre-RoPE, v fp16 [B,H,T,128].
- * Same split-K engine and RoPE as reskv_decode, out fp16 [B*Hq,128]. */
+ * q fp16 [B*Hq,128] pre-RoPE, k fp16 [B,H,*,128] pre-RoPE, v fp16 [B,H,*,128]:
+ * the first T tokens of rows of t_stride tokens (t_stride<=0: T), so that a
+ * preallocated cache is read in place.  Same split-K engine and RoPE as
+ * reskv_decode_rope (rope_table may be NULL), out fp16 [B*Hq,128]. */
 int reskv_decode_dense(const void* q, const void* k, const void* v, const float* inv_freq,
-                       int B, int Hq, int H, int T, int start_pos, int pos_q, float scaling,
-                       int splits, void* out, float* m, float* l, void* workspace,
-                       int64_t workspace_bytes, void* stream);
+                       const float* rope_table, int B, int Hq, int H, int T, int t_stride, int start_pos,
+                       int pos_q, float scaling, int splits, void* out, float* m, float* l,
+                       void* workspace, int64_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

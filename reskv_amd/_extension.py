@@ -81,8 +81,11 @@ _ROPE_TABLES = {}
 _ROPE_TABLE_LIMIT = 16
 
 
-def _rope_table(freq, key, positions):
-    """fp32 [P, 128] table covering positions [0, positions), P a power of two."""
+def _rope_table(freq, key, positions, source=None):
+    """fp32 [P, 128] table covering positions [0, positions), P a power of two.
+
+    ``source`` is the tensor whose address is part of ``key``; the cache keeps
+    it alive so that the address cannot be reused by other frequencies."""
     entry = _ROPE_TABLES.get(key)
     if entry is not None and entry[0].shape[0] >= positions:
         return entry[0]
@@ -93,8 +96,18 @@ def _rope_table(freq, key, positions):
                    "rope_table")
     if len(_ROPE_TABLES) >= _ROPE_TABLE_LIMIT:
         _ROPE_TABLES.pop(next(iter(_ROPE_TABLES)))
-    _ROPE_TABLES[key] = (table, freq)  # keeps the source tensor alive so its address is not reused
+    _ROPE_TABLES[key] = (table, source)
     return table
+
+
+def _rope(inv_freq, rope_base, dev, positions):
+    """(frequencies, table) for the caller's inv_freq [64] or the theta-derived set."""
+    freq = _frequencies(inv_freq, rope_base, dev)
+    if inv_freq is not None and inv_freq.numel():
+        key, source = (dev, inv_freq.data_ptr(), inv_freq._version), inv_freq
+    else:
+        key, source = (dev, "theta", float(rope_base)), None
+    return freq, _rope_table(freq, key, positions, source)
 
 
 def _frequencies(inv_freq, rope_base, device):
@@ -259,12 +272,7 @@ def _decode(Q, kdesc, vdesc, keep, nh_kv, nh, start_pos, pos_q, rope_base, scali
     _require(ids.shape[0] == b * nh_kv, "cache batch-head count does not match Q")
     t = ids.shape[1]
     dev = Q.device
-    freq = _frequencies(inv_freq, rope_base, dev)
-    if inv_freq is not None and inv_freq.numel():
-        key = (dev, inv_freq.data_ptr(), inv_freq._version)
-    else:
-        key = (dev, "theta", float(rope_base))
-    table = _rope_table(freq, key, int(start_pos) + t)
+    freq, table = _rope(inv_freq, rope_base, dev, int(start_pos) + t)
     L = _lib.lib()
     out = _empty((bnh, 128), torch.float16, dev)
     m = _empty((bnh,), torch.float32, dev)
@@ -276,6 +284,75 @@ def _decode(Q, kdesc, vdesc, keep, nh_kv, nh, start_pos, pos_q, rope_base, scali
                                        m.data_ptr(), l.data_ptr(), ws.data_ptr(), ws.numel(), _stream(dev)),
                    "decode")
     return [out, m, l] if return_stats else [out]
+
+
+def cache_descriptors(cache):
+    """C descriptors of a CompressedKV's key and value tensors (the format the
+    family ops derive from the plan) and the tensors they point into."""
+    plan = cache.key.plan
+    out, keep = [], []
+    for t in (cache.key, cache.value):
+        c, i, p, m, sc = t._native
+        if plan.bits == 16 and plan.layout == "unstructured":
+            fmt, bits, sc = _lib.FMT_BITMAP, 16, None
+        elif plan.bits == 16:
+            fmt, bits, sc = (_lib.FMT_STRUCT16 if plan.layout == "structured" else _lib.FMT_TILED), 16, None
+        elif plan.layout == "structured":
+            fmt, bits = _lib.FMT_STRUCT_INT4, 4
+        else:
+            fmt, bits, m = _lib.FMT_QUANT, int(plan.bits), None
+        out.append(_ctensor(c, i, p, m, sc, fmt, bits))
+        keep.extend(x for x in (c, i, p, m, sc) if x is not None)
+    return out[0], out[1], tuple(keep)
+
+
+class StepDecoder:
+    """Repeated decode steps of one layer against a fixed compressed history and
+    a dense ring of recent tokens, without per-call validation or allocation.
+
+    Descriptors, the RoPE table, the split workspace and the outputs are made
+    once for a CompressedKV; each ``run`` issues the fused decode
+    (``reskv_decode_rope``) and the in-place ring merge
+    (``reskv_merge_recent_qk`` over rows of ``ring_stride`` tokens).  The result
+    equals ``attention(query, cache, position=..., recent=(...))``."""
+
+    def __init__(self, cache, num_q_heads, scaling, inv_freq=None, rope_theta=500000.0, splits=0):
+        self.cache = cache
+        self.kdesc, self.vdesc, self.keep = cache_descriptors(cache)
+        dev = cache.key.payload.device
+        self.dev = dev
+        self.b, self.kh = cache.key.centroids.shape[:2]
+        self.nh = int(num_q_heads)
+        self.t = cache.seq_len
+        self.scaling = float(scaling)
+        self.freq, self.table = _rope(inv_freq, rope_theta, dev, self.t)
+        L = _lib.lib()
+        self.splits = int(splits)
+        self.ws = _workspace(L.reskv_decode_workspace_bytes(self.b, self.nh, self.kh, self.t, self.splits), dev)
+        rows = self.b * self.nh
+        self.out = torch.empty((rows, 128), dtype=torch.float16, device=dev)
+        self.m = torch.empty((rows,), dtype=torch.float32, device=dev)
+        self.l = torch.empty((rows,), dtype=torch.float32, device=dev)
+        self.merged = torch.empty((rows, 128), dtype=torch.float16, device=dev)
+
+    def run(self, query, position, query_rot=None, ring_k=None, ring_v=None, ring_len=0, ring_stride=0):
+        """query fp16 [B, Hq, 1, 128] pre-RoPE (contiguous); ring_k/ring_v fp16
+        [B, Hk, ring_stride, 128] buffers whose first ring_len tokens are the
+        recent window (rotated K, V); query_rot its rotated query.  Returns
+        fp16 [B, Hq, 1, 128] (a buffer reused by the next call)."""
+        L = _lib.lib()
+        stream = _stream(self.dev)
+        _lib.check(L.reskv_decode_rope(query.data_ptr(), self.kdesc, self.vdesc, self.freq.data_ptr(),
+                                       self.table.data_ptr(), self.b, self.nh, self.kh, self.t, 0, int(position),
+                                       self.scaling, self.splits, self.out.data_ptr(), self.m.data_ptr(),
+                                       self.l.data_ptr(), self.ws.data_ptr(), self.ws.numel(), stream), "decode")
+        if ring_len <= 0:
+            return self.out.view(self.b, self.nh, 1, 128)
+        _lib.check(L.reskv_merge_recent_qk(self.out.data_ptr(), self.m.data_ptr(), self.l.data_ptr(),
+                                           query_rot.data_ptr(), ring_k.data_ptr(), ring_v.data_ptr(), self.b,
+                                           self.nh, self.kh, int(ring_len), int(ring_stride), self.scaling,
+                                           self.merged.data_ptr(), stream), "merge_recent")
+        return self.merged.view(self.b, self.nh, 1, 128)
 
 
 def _make_cluster_mass():
@@ -385,7 +462,7 @@ def _make_attention(plan):
         with torch.cuda.device(dev):
             _lib.check(_lib.lib().reskv_merge_recent_qk(
                 comp_out.data_ptr(), comp_m.data_ptr(), comp_l.data_ptr(), _ptr(Q_rope), _ptr(k_recent),
-                _ptr(v_recent), b, nh, nh_kv, tr, float(scaling), out.data_ptr(), _stream(dev)), "merge_recent")
+                _ptr(v_recent), b, nh, nh_kv, tr, tr, float(scaling), out.data_ptr(), _stream(dev)), "merge_recent")
         return out
 
     return SimpleNamespace(decode_fp16=_per_token(False), decode_int4=_per_token(True),
@@ -418,20 +495,29 @@ def load_extension(family: str, plan: KernelPlan | None = None, device_index: in
 def dense_decode(q, k, v, inv_freq, *, position, start_position=0, scaling=None, splits=0):
     """Dense fp16 decode attention baseline on the same split-K engine.
 
-    q fp16 [B, Hq, 1, 128] pre-RoPE; k, v fp16 [B, H, T, 128] (k pre-RoPE).
+    q fp16 [B, Hq, 1, 128] pre-RoPE; k, v fp16 [B, H, T, 128] (k pre-RoPE),
+    contiguous or the first T tokens of a preallocated [B, H, Tmax, 128] cache.
     Returns fp16 [B, Hq, 1, 128].
     """
     _require(q.dtype == torch.float16 and k.dtype == torch.float16 and v.dtype == torch.float16, "fp16 inputs")
-    dev = _dev_check(q, k, v)
+    dev = _dev_check(q, contiguous=True)
+    _dev_check(q, k, v, contiguous=False)
     b, hq = q.shape[:2]
     h, t = k.shape[1], k.shape[2]
+    _require(v.shape == k.shape and k.dim() == 4 and k.shape[3] == 128, "K and V must be [B, H, T, 128]")
+    ts = k.stride(1) // 128
+    for x in (k, v):
+        _require(x.stride(3) == 1 and x.stride(2) == 128 and x.stride(1) == ts * 128
+                 and (x.shape[0] == 1 or x.stride(0) == h * x.stride(1)),
+                 "K/V must be contiguous or a token prefix of a [B, H, Tmax, 128] buffer")
     scale = 128 ** -0.5 if scaling is None else float(scaling)
-    freq = _frequencies(inv_freq, 500000.0, dev)
+    freq, table = _rope(inv_freq, 500000.0, dev, int(start_position) + t)
     L = _lib.lib()
     out = _empty((b * hq, 128), torch.float16, dev)
     ws = _workspace(L.reskv_decode_workspace_bytes(b, hq, h, t, int(splits)), dev)
     with torch.cuda.device(dev):
-        _lib.check(L.reskv_decode_dense(q.data_ptr(), k.data_ptr(), v.data_ptr(), freq.data_ptr(), b, hq, h, t,
-                                        int(start_position), int(position), scale, int(splits), out.data_ptr(),
-                                        None, None, ws.data_ptr(), ws.numel(), _stream(dev)), "decode_dense")
+        _lib.check(L.reskv_decode_dense(q.data_ptr(), k.data_ptr(), v.data_ptr(), freq.data_ptr(), table.data_ptr(),
+                                        b, hq, h, t, ts, int(start_position), int(position), scale, int(splits),
+                                        out.data_ptr(), None, None, ws.data_ptr(), ws.numel(), _stream(dev)),
+                   "decode_dense")
     return out.reshape(b, hq, 1, 128)

@@ -21,6 +21,7 @@ the model patch and without a particular transformers version.
 
 import torch
 
+from ._extension import StepDecoder
 from .compression import _compress_group, compress
 from .config import ResKVKernelConfig
 from .tensors import CompressedKV, CompressedTensor
@@ -113,6 +114,7 @@ class ResKVLayerCache:
         self.is_initialized = False
         self._k = self._v = None
         self._view = None
+        self._stepper = None
 
     # -- state ---------------------------------------------------------------
     @property
@@ -183,6 +185,24 @@ class ResKVLayerCache:
         self.length += q_len
         return self.keys[:, :, : self.live], self.values[:, :, : self.live]
 
+    # -- decode attention (reskv/models/llama.py:45-60) ------------------------
+    def attend(self, query, query_rot, *, scaling, inv_freq=None, rope_theta=500000.0):
+        """Attention of the newest token (after ``update``) over the compressed
+        history and the dense ring, as the model patch computes it with
+        ``attention(query, self.compressed, position=self.length - 1,
+        recent=(query_rot, ring K, ring V))``.  Repeated steps reuse the
+        descriptors, RoPE table and buffers until a group compression changes
+        the history; the ring is read in place.  query / query_rot fp16
+        [B, Hq, 1, 128] (pre-RoPE / rotated, contiguous).  The returned tensor
+        is reused by the next call."""
+        cv = self.compressed
+        if cv is None:
+            raise ValueError("no compressed history yet; attend over the ring densely")
+        if self._stepper is None or self._stepper.cache is not cv:
+            self._stepper = StepDecoder(cv, query.shape[1], scaling, inv_freq, rope_theta)
+        return self._stepper.run(query, self.length - 1, query_rot, self.keys, self.values, self.live,
+                                 self.keys.shape[2])
+
     # -- queries -------------------------------------------------------------
     def get_seq_length(self, *_):
         return self.length
@@ -198,6 +218,7 @@ class ResKVLayerCache:
     def reset(self):
         self.keys = self.values = self.raw_keys = None
         self._k = self._v = self._view = None
+        self._stepper = None
         self.length = self.live = 0
         self.plan = None
         self.is_initialized = False

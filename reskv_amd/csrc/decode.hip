@@ -889,35 +889,81 @@ __global__ void __launch_bounds__(kMergeThreads) decode_merge_kernel(
 
 // Joint softmax of a normalised compressed result (m, l) with Tr recent tokens
 // whose scaled scores are given (scores != null) or computed from q_rope/k.
-__global__ void __launch_bounds__(64) merge_recent_kernel(
+// Recent K/V rows of (batch, head) block bh start at token bh * rs.
+// One 128-thread workgroup per (batch, query head): the window is taken in
+// chunks of 128 tokens, thread t scoring token t of the chunk (a full 128-dim
+// dot product against the query in LDS) and then owning channel t of the
+// weighted value sum; chunks combine by online rescaling (natural-log units).
+constexpr int kRecentThreads = 128;
+
+__device__ __forceinline__ float block_max128(float v, float* red) {
+    v = wave_max(v);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    v = fmaxf(red[0], red[1]);
+    __syncthreads();
+    return v;
+}
+__device__ __forceinline__ float block_sum128(float v, float* red) {
+    v = wave_sum(v);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    v = red[0] + red[1];
+    __syncthreads();
+    return v;
+}
+
+__global__ void __launch_bounds__(kRecentThreads) merge_recent_kernel(
     const uint16_t* __restrict__ comp_out, const float* __restrict__ comp_m, const float* __restrict__ comp_l,
     const float* __restrict__ scores, const uint16_t* __restrict__ q_rope, const uint16_t* __restrict__ k_recent,
-    const uint16_t* __restrict__ v_recent, int Hq, int H, int Tr, float scaling, uint16_t* __restrict__ out) {
+    const uint16_t* __restrict__ v_recent, int Hq, int H, int Tr, int rs, float scaling,
+    uint16_t* __restrict__ out) {
+    __shared__ float s_q[kDim];
+    __shared__ float s_p[kRecentThreads];
+    __shared__ float s_red[kRecentThreads / kWave];
     const long bq = blockIdx.x;
-    const int lane = threadIdx.x;
+    const int tid = threadIdx.x;
     const int G = Hq / H;
     const long b = bq / Hq, hq = bq % Hq;
     const long bh = b * H + hq / G;
-    float qa = 0.0f, qb = 0.0f;
-    if (scores == nullptr) {
-        qa = h2f(q_rope[bq * kDim + lane]);
-        qb = h2f(q_rope[bq * kDim + lane + 64]);
-    }
-    float m = -INFINITY, l = 0.0f, a0 = 0.0f, a1 = 0.0f;
-    for (int t = 0; t < Tr; ++t) {
-        const long vrow = (bh * Tr + t) * kDim;
-        float s;
-        if (scores != nullptr) {
-            s = scores[bq * Tr + t];
-        } else {
-            s = wave_sum(qa * h2f(k_recent[vrow + lane]) + qb * h2f(k_recent[vrow + lane + 64])) * scaling;
+    if (scores == nullptr) s_q[tid] = h2f(q_rope[bq * kDim + tid]) * scaling;
+    __syncthreads();
+    float m = -INFINITY, l = 0.0f, acc = 0.0f;  // acc: channel tid
+    for (int c0 = 0; c0 < Tr; c0 += kRecentThreads) {
+        const int t = c0 + tid;
+        float s = -INFINITY;
+        if (t < Tr) {
+            if (scores != nullptr) {
+                s = scores[bq * Tr + t];
+            } else {
+                const uint4* kr = reinterpret_cast<const uint4*>(k_recent + (bh * rs + t) * kDim);
+                float d = 0.0f;
+#pragma unroll
+                for (int i = 0; i < kDim / 8; ++i) {
+                    const uint4 w = kr[i];
+                    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        d = fmaf(s_q[8 * i + 2 * j], h2f((uint16_t)(ws[j] & 0xFFFFu)), d);
+                        d = fmaf(s_q[8 * i + 2 * j + 1], h2f((uint16_t)(ws[j] >> 16)), d);
+                    }
+                }
+                s = d;
+            }
         }
-        const float mn = fmaxf(m, s);
-        const float alpha = expf(m - mn), p = expf(s - mn);
-        l = l * alpha + p;
-        a0 = a0 * alpha + p * h2f(v_recent[vrow + lane]);
-        a1 = a1 * alpha + p * h2f(v_recent[vrow + lane + 64]);
+        const float mn = fmaxf(m, block_max128(s, s_red));
+        const float p = t < Tr ? expf(s - mn) : 0.0f;
+        s_p[tid] = p;
+        const float ps = block_sum128(p, s_red);  // its barriers also publish s_p
+        const float alpha = expf(m - mn);  // 0 for the first chunk (m = -inf, mn finite)
+        l = l * alpha + ps;
+        const int n = min(kRecentThreads, Tr - c0);
+        const uint16_t* vr = v_recent + (bh * rs + c0) * kDim + tid;
+        float a = 0.0f;
+        for (int j = 0; j < n; ++j) a = fmaf(s_p[j], h2f(vr[(long)j * kDim]), a);
+        acc = acc * alpha + a;
         m = mn;
+        __syncthreads();  // s_p reads done before the next chunk writes it
     }
     const float cm = comp_m[bq], cl = comp_l[bq];
     const float jm = fmaxf(cm, m);
@@ -925,8 +971,7 @@ __global__ void __launch_bounds__(64) merge_recent_kernel(
     const float wr = Tr > 0 ? expf(m - jm) : 0.0f;
     const float denom = wc + l * wr;
     const float inv = denom > 0.0f ? 1.0f / denom : 0.0f;
-    out[bq * kDim + lane] = f2h((h2f(comp_out[bq * kDim + lane]) * wc + a0 * wr) * inv);
-    out[bq * kDim + lane + 64] = f2h((h2f(comp_out[bq * kDim + lane + 64]) * wc + a1 * wr) * inv);
+    out[bq * kDim + tid] = f2h((h2f(comp_out[bq * kDim + tid]) * wc + acc * wr) * inv);
 }
 
 // ---------------------------------------------------------------------------
@@ -1160,14 +1205,16 @@ extern "C" int reskv_decode(const void* q, const reskv_ctensor* k, const reskv_c
 }
 
 extern "C" int reskv_decode_dense(const void* q, const void* k, const void* v, const float* inv_freq,
-                                  int B, int Hq, int H, int T, int start_pos, int pos_q, float scaling,
-                                  int splits, void* out, float* m, float* l, void* workspace,
-                                  int64_t workspace_bytes, void* stream) {
+                                  const float* rope_table, int B, int Hq, int H, int T, int t_stride, int start_pos,
+                                  int pos_q, float scaling, int splits, void* out, float* m, float* l,
+                                  void* workspace, int64_t workspace_bytes, void* stream) {
     RESKV_REQUIRE(k && v, "null K/V pointer");
     RESKV_REQUIRE((((uintptr_t)k | (uintptr_t)v) & 15u) == 0, "K and V must be 16-byte aligned");
-    const DTensor kd{nullptr, nullptr, (const uint8_t*)k, nullptr, nullptr, 1, kDim, 2 * kDim, T, 1};
-    const DTensor vd{nullptr, nullptr, (const uint8_t*)v, nullptr, nullptr, 1, kDim, 2 * kDim, T, 1};
-    return run_decode(q, D_DENSE, kd, D_DENSE, vd, inv_freq, nullptr, B, Hq, H, T, start_pos, pos_q, scaling,
+    const int ts = t_stride > 0 ? t_stride : T;
+    RESKV_REQUIRE(ts >= T, "row stride shorter than the sequence");
+    const DTensor kd{nullptr, nullptr, (const uint8_t*)k, nullptr, nullptr, 1, kDim, 2 * kDim, ts, 1};
+    const DTensor vd{nullptr, nullptr, (const uint8_t*)v, nullptr, nullptr, 1, kDim, 2 * kDim, ts, 1};
+    return run_decode(q, D_DENSE, kd, D_DENSE, vd, inv_freq, rope_table, B, Hq, H, T, start_pos, pos_q, scaling,
                       splits, out, m, l, workspace, workspace_bytes, stream);
 }
 
@@ -1201,20 +1248,24 @@ extern "C" int reskv_merge_recent_scores(const void* comp_out, const float* comp
     RESKV_REQUIRE(comp_out && comp_m && comp_l && out, "null pointer argument");
     RESKV_REQUIRE(B > 0 && H > 0 && Hq % H == 0 && Tr >= 0, "bad recent-merge sizes");
     RESKV_REQUIRE(Tr == 0 || (scores && v_recent), "null recent scores/values");
-    hipLaunchKernelGGL(merge_recent_kernel, dim3(B * Hq), dim3(64), 0, (hipStream_t)stream,
+    hipLaunchKernelGGL(merge_recent_kernel, dim3(B * Hq), dim3(kRecentThreads), 0, (hipStream_t)stream,
                        (const uint16_t*)comp_out, comp_m, comp_l, scores, nullptr, nullptr,
-                       (const uint16_t*)v_recent, Hq, H, Tr, 1.0f, (uint16_t*)out);
+                       (const uint16_t*)v_recent, Hq, H, Tr, Tr, 1.0f, (uint16_t*)out);
     return reskv_host::check_launch("merge_recent_kernel");
 }
 
 extern "C" int reskv_merge_recent_qk(const void* comp_out, const float* comp_m, const float* comp_l,
                                      const void* q_rope, const void* k_recent, const void* v_recent, int B,
-                                     int Hq, int H, int Tr, float scaling, void* out, void* stream) {
+                                     int Hq, int H, int Tr, int r_stride, float scaling, void* out,
+                                     void* stream) {
     RESKV_REQUIRE(comp_out && comp_m && comp_l && out, "null pointer argument");
     RESKV_REQUIRE(B > 0 && H > 0 && Hq % H == 0 && Tr >= 0, "bad recent-merge sizes");
+    const int rs = r_stride > 0 ? r_stride : Tr;
+    RESKV_REQUIRE(rs >= Tr, "recent row stride shorter than the window");
     RESKV_REQUIRE(Tr == 0 || (q_rope && k_recent && v_recent), "null recent tensors");
-    hipLaunchKernelGGL(merge_recent_kernel, dim3(B * Hq), dim3(64), 0, (hipStream_t)stream,
+    RESKV_REQUIRE(Tr == 0 || ((((uintptr_t)k_recent) & 15u) == 0), "recent K must be 16-byte aligned");
+    hipLaunchKernelGGL(merge_recent_kernel, dim3(B * Hq), dim3(kRecentThreads), 0, (hipStream_t)stream,
                        (const uint16_t*)comp_out, comp_m, comp_l, nullptr, (const uint16_t*)q_rope,
-                       (const uint16_t*)k_recent, (const uint16_t*)v_recent, Hq, H, Tr, scaling, (uint16_t*)out);
+                       (const uint16_t*)k_recent, (const uint16_t*)v_recent, Hq, H, Tr, rs, scaling, (uint16_t*)out);
     return reskv_host::check_launch("merge_recent_kernel");
 }

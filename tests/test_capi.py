@@ -43,7 +43,7 @@ def test_null_pointers_are_rejected_without_a_gpu():
     assert "null" in _err(lib.reskv_compress_fp16(None, None, None, None, None, 1, 1, 1, 1, 32, 1, None))
     assert "null" in _err(lib.reskv_compress_bitmap(None, None, None, None, None, 1, 1, 1, 1, 32, None))
     assert "null" in _err(lib.reskv_kmeans(None, None, None, None, 1, 1, 1, 1, 0, None, 0, None))
-    assert "null" in _err(lib.reskv_merge_recent_qk(None, None, None, None, None, None, 1, 4, 1, 1, 1.0, None,
+    assert "null" in _err(lib.reskv_merge_recent_qk(None, None, None, None, None, None, 1, 4, 1, 1, 0, 1.0, None,
                                                     None))
 
 

@@ -95,3 +95,26 @@ def test_decode_over_capacity_views_with_ring(device, bits, sparsity):
     out = attention(q, layer.compressed, position=pos, inv_freq=freq, recent=ring)
     ref = expected_attention(q, layer.compressed, position=pos, inv_freq=freq, recent=ring)
     assert float(np.abs(np_(out).astype(np.float64) - ref).max()) <= ATOL
+
+
+@pytest.mark.parametrize("bits,sparsity", [(16, 0.5), (16, 0.75), (4, 0.5)])
+def test_attend_fast_path_equals_attention(device, bits, sparsity):
+    """layer.attend (cached descriptors, ring read in place) == attention(..., recent=ring), across group
+    compressions that change the history."""
+    cfg = ResKVKernelConfig(bits=bits, sparsity=sparsity, num_clusters=8, max_clusters=12, group_size=32,
+                            recent_size=16)
+    k, v = _inputs(220, device, seed=9, b=2, h=2)
+    g = seeded(10)
+    freq = (500000.0 ** (-torch.arange(64).float() / 64)).to(device)
+    layer = ResKVLayerCache(cfg)
+    layer.update(k[:, :, :120], v[:, :, :120], {"raw_keys": k[:, :, :120]})
+    for t in range(120, 220):
+        layer.update(k[:, :, t:t + 1], v[:, :, t:t + 1], {"raw_keys": k[:, :, t:t + 1]})
+        if t % 7:
+            continue
+        q = torch.randn(2, 8, 1, 128, generator=g).half().to(device)
+        qr = torch.randn(2, 8, 1, 128, generator=g).half().to(device)
+        fast = layer.attend(q, qr, scaling=0.1, inv_freq=freq).clone()
+        ref = attention(q, layer.compressed, position=layer.length - 1, inv_freq=freq, scaling=0.1,
+                        recent=(qr, layer.keys[:, :, :layer.live], layer.values[:, :, :layer.live]))
+        assert torch.equal(fast, ref), t

@@ -188,6 +188,21 @@ def test_dense_baseline_decode(device):
     assert _max_err(out, ref) <= ATOL
 
 
+def test_dense_baseline_decode_reads_cache_prefix(device):
+    """A token prefix of a preallocated [B, H, Tmax, 128] cache equals the same tokens packed."""
+    from reskv_amd._extension import dense_decode
+
+    k, v, q = outlier_kv(2, 8, 300, seed=5, gqa=4)
+    freq = theta_freq()
+    kbuf = torch.zeros(2, 8, 512, 128, dtype=torch.float16, device=k.device)
+    vbuf = torch.zeros_like(kbuf)
+    kbuf[:, :, :300] = k
+    vbuf[:, :, :300] = v
+    out = dense_decode(q, kbuf[:, :, :300], vbuf[:, :, :300], freq, position=310)
+    ref = dense_decode(q, k, v, freq, position=310)
+    assert torch.equal(out, ref)
+
+
 def test_query_position_before_cache_rejected(device):
     k, v, q, c = reference_test_inputs(t=64)
     cache = compress(k, v, clustering=c)

@@ -1,0 +1,73 @@
+"""End-to-end decode harness (random-init Llama shape) at a tiny size."""
+
+import pytest
+import torch
+
+from reskv_amd import ResKVKernelConfig
+from reskv_amd.llama import GreedyDecoder, LlamaShape, RandomLlama, llama3_inv_freq
+
+TINY = LlamaShape(layers=2, hidden=512, heads=4, kv_heads=1, ffn=1024, vocab=1000)
+
+
+def _run(mode, steps=70, prompt=256, batch=2):
+    model = RandomLlama(TINY, "cuda", seed=1)
+    ids = torch.randint(128, TINY.vocab, (batch, prompt), generator=torch.Generator().manual_seed(3)).cuda()
+    cfg = ResKVKernelConfig(sparsity=0.75, num_clusters=8, kmeans_iterations=4)
+    dec = GreedyDecoder(model, batch, prompt, steps, mode, cfg)
+    keep = {}
+
+    def sink(layer, raw_k, rot_k, v):
+        keep[layer] = (raw_k.clone(), v.clone())
+        dec.absorb(layer, raw_k, rot_k, v)
+
+    first = model.prefill(ids, sink, q_rows=64)
+    dec.start(first)
+    toks = [dec.step().clone() for _ in range(steps)]
+    torch.cuda.synchronize()
+    return model, dec, keep, torch.stack(toks)
+
+
+def test_llama3_frequencies_match_closed_form():
+    inv = llama3_inv_freq(LlamaShape())
+    base = 1.0 / (500000.0 ** (torch.arange(0, 128, 2).float() / 128))
+    assert torch.allclose(inv[:8], base[:8])  # short wavelengths untouched
+    assert torch.allclose(inv[-4:], base[-4:] / 8.0)  # long wavelengths divided by the factor
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("mode", ["reskv", "dense"])
+def test_decode_runs_and_keeps_cache_consistent(device, mode):
+    model, dec, _, toks = _run(mode)
+    assert toks.shape == (70, 2)
+    assert int(toks.min()) >= 0 and int(toks.max()) < TINY.vocab
+    assert torch.isfinite(dec.x.float()).all()
+    if mode == "reskv":
+        for layer in dec.caches:
+            assert layer.get_seq_length() == 256 + 70
+            assert layer.compressed.seq_len + layer.live == layer.get_seq_length()
+            assert layer.live <= 96
+
+
+@pytest.mark.gpu
+def test_dense_first_step_attention_matches_fp32(device):
+    """The harness's dense attention (strided cache, in-kernel RoPE) against fp32 attention."""
+    model = RandomLlama(TINY, "cuda", seed=2)
+    ids = torch.randint(128, TINY.vocab, (2, 128), generator=torch.Generator().manual_seed(4)).cuda()
+    dec = GreedyDecoder(model, 2, 128, 4, "dense")
+    first = model.prefill(ids, dec.absorb, q_rows=64)
+    dec.start(first)
+    dec.capture()
+    dec.pos_buf.fill_(dec.pos)
+    dec.graphs[0][0].replay()
+    dec._attend(0)
+    t = dec.pos + 1
+    cos, sin = model.rope_tables(t)
+    k = dec.kc[0][:, :, :t].float()
+    kr = torch.cat((k[..., :64] * cos - k[..., 64:] * sin, k[..., 64:] * cos + k[..., :64] * sin), -1)
+    v = dec.vc[0][:, :, :t].float()
+    q = dec.qr.float()  # [B, Hq, 128] rotated at the step's position
+    kr = kr.repeat_interleave(4, dim=1)
+    v = v.repeat_interleave(4, dim=1)
+    w = torch.softmax(torch.einsum("bhd,bhtd->bht", q, kr) * model.scaling, -1)
+    ref = torch.einsum("bht,bhtd->bhd", w, v)
+    assert (dec.attn.float() - ref).abs().max().item() <= 2e-3
