@@ -511,12 +511,14 @@ def dense_decode(q, k, v, inv_freq, *, position, start_position=0, scaling=None,
                  and (x.shape[0] == 1 or x.stride(0) == h * x.stride(1)),
                  "K/V must be contiguous or a token prefix of a [B, H, Tmax, 128] buffer")
     scale = 128 ** -0.5 if scaling is None else float(scaling)
-    freq, table = _rope(inv_freq, 500000.0, dev, int(start_position) + t)
+    # sin/cos evaluated in-kernel (no table): the dense stream leaves VALU time to
+    # spare, while table reads would compete with it for the caches
+    freq = _frequencies(inv_freq, 500000.0, dev)
     L = _lib.lib()
     out = _empty((b * hq, 128), torch.float16, dev)
     ws = _workspace(L.reskv_decode_workspace_bytes(b, hq, h, t, int(splits)), dev)
     with torch.cuda.device(dev):
-        _lib.check(L.reskv_decode_dense(q.data_ptr(), k.data_ptr(), v.data_ptr(), freq.data_ptr(), table.data_ptr(),
+        _lib.check(L.reskv_decode_dense(q.data_ptr(), k.data_ptr(), v.data_ptr(), freq.data_ptr(), None,
                                         b, hq, h, t, ts, int(start_position), int(position), scale, int(splits),
                                         out.data_ptr(), None, None, ws.data_ptr(), ws.numel(), _stream(dev)),
                    "decode_dense")

@@ -36,6 +36,9 @@ def build_command(out: Path):
         "-Wno-unused-function",
         # packed fp32 VALU forms are kept out of every kernel
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        # matrix-core accumulators in ordinary VGPRs: accumulators that the VALU
+        # rescales are then not copied between the two register files
+        "-mllvm", "-amdgpu-mfma-vgpr-form",
         f"-I{HERE.parent / 'include'}",
         "-o", str(out),
     ]

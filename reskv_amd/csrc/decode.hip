@@ -116,37 +116,54 @@ struct Prefetch {
     float sc;
 };
 
-// Loads the raw bytes of tokens [row0, row0 + n) of one tensor (row0 = bh*T + t);
-// bytes past the n tokens are zero, so padded tokens decode to zero residuals.
+// The bytes of one wave's token range [t0, t1) of one tensor as raw buffer
+// resources: loads past the range return zero (hardware range check), so a
+// partial last tile decodes to zero residuals without masks or zero fills.
+constexpr int kBufferWord3 = 0x00020000;  // gfx9 raw buffer, 32-bit data
+
 template <int F>
-__device__ __forceinline__ void prefetch(const DTensor& X, long row0, int n, int lane, Prefetch<F>& P) {
+struct WaveSrc {
+    __amdgpu_buffer_rsrc_t pay, meta, ids, scale;
+};
+
+template <int F>
+__device__ __forceinline__ WaveSrc<F> wave_src(const DTensor& X, long row0, int count) {
     using Tr = Traits<F>;
-    const int per_tok = X.pb >> 4;
-    const int pieces = n * per_tok;
-    const uint4* src = reinterpret_cast<const uint4*>(X.payload + row0 * X.pb);
+    WaveSrc<F> w;
+    w.pay = __builtin_amdgcn_make_buffer_rsrc((void*)(X.payload + row0 * X.pb), 0, count * X.pb, kBufferWord3);
+    w.meta = w.ids = w.scale = w.pay;
+    if constexpr (Tr::MB > 0)
+        w.meta = __builtin_amdgcn_make_buffer_rsrc((void*)(X.meta + row0 * Tr::MB), 0, count * Tr::MB, kBufferWord3);
+    if constexpr (Tr::CENT)
+        w.ids = __builtin_amdgcn_make_buffer_rsrc((void*)(X.ids + row0), 0, count, kBufferWord3);
+    if constexpr (Tr::SC)
+        w.scale = __builtin_amdgcn_make_buffer_rsrc((void*)(X.scale + row0), 0, count * 2, kBufferWord3);
+    return w;
+}
+
+// Loads the raw bytes of the tile starting `off` tokens into the wave's range.
+template <int F>
+__device__ __forceinline__ void prefetch(const WaveSrc<F>& W, int pb, int off, int lane, Prefetch<F>& P) {
+    using Tr = Traits<F>;
+    constexpr int kOut = 0x7FFFFFF0;  // an offset past every range: the load returns zero
+    const int per_tok = pb >> 4;
 #pragma unroll
     for (int i = 0; i < Tr::PQ; ++i) {
         const int q = lane + kWave * i;
-        P.pay[i] = q < pieces ? src[q] : make_uint4(0, 0, 0, 0);
+        const int o = q < kTile * per_tok ? off * pb + 16 * q : kOut;
+        P.pay[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(W.pay, o, 0, 0));
     }
-    P.meta = make_uint4(0, 0, 0, 0);
+    const int tok = lane < kTile ? off + lane : -1;
     if constexpr (Tr::MB == 16) {
-        if (lane < n) P.meta = reinterpret_cast<const uint4*>(X.meta + row0 * 16)[lane];
+        P.meta = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(W.meta, tok >= 0 ? tok * 16 : kOut, 0, 0));
     } else if constexpr (Tr::MB == 8) {
-        if (lane < n) {
-            const uint2 m = reinterpret_cast<const uint2*>(X.meta + row0 * 8)[lane];
-            P.meta.x = m.x;
-            P.meta.y = m.y;
-        }
+        const uint2 m = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(W.meta, tok >= 0 ? tok * 8 : kOut, 0, 0));
+        P.meta = make_uint4(m.x, m.y, 0, 0);
     }
-    P.id = 0;
-    if constexpr (Tr::CENT) {
-        if (lane < n) P.id = X.ids[row0 + lane];
-    }
-    P.sc = 0.0f;
-    if constexpr (Tr::SC) {
-        if (lane < n) P.sc = h2f(X.scale[row0 + lane]);
-    }
+    if constexpr (Tr::CENT)
+        P.id = (int)(int8_t)__builtin_amdgcn_raw_buffer_load_b8(W.ids, tok >= 0 ? tok : kOut, 0, 0);
+    if constexpr (Tr::SC)
+        P.sc = h2f(__builtin_amdgcn_raw_buffer_load_b16(W.scale, tok >= 0 ? tok * 2 : kOut, 0, 0));
 }
 
 // Stage layout (bytes): payload [16][pb + 16] | meta [16][MB] | ids int32[16] |
@@ -488,7 +505,8 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
     const long bh = (long)b * P.H + h;
     const int s0 = (int)(((long)split * P.T) / P.splits);
     const int s1 = (int)(((long)(split + 1) * P.T) / P.splits);
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar registers
     const int t = lane & 15, grp = lane >> 4;  // decode: token of the tile, channel group
     const int hj = lane & 3;                     // query head of this lane within a set
     const int stok = 4 * ((lane >> 2) & 3) + (lane >> 4);  // token of this lane's score
@@ -579,12 +597,13 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
     __syncthreads();
 
     const int ntiles = (t1 - t0 + kTile - 1) / kTile;
-    Prefetch<KF> pk;
-    Prefetch<VF> pv;
+    const WaveSrc<KF> wk = wave_src<KF>(P.k, bh * P.k.ts + t0, t1 - t0);
+    const WaveSrc<VF> wv = wave_src<VF>(P.v, bh * P.v.ts + t0, t1 - t0);
+    Prefetch<KF> pk{};
+    Prefetch<VF> pv{};
     if (ntiles > 0) {
-        const int n = min(kTile, t1 - t0);
-        prefetch<KF>(P.k, bh * P.k.ts + t0, n, lane, pk);
-        prefetch<VF>(P.v, bh * P.v.ts + t0, n, lane, pv);
+        prefetch<KF>(wk, P.k.pb, 0, lane, pk);
+        prefetch<VF>(wv, P.v.pb, 0, lane, pv);
     }
     for (int tile = 0; tile < ntiles; ++tile) {
         const int tb = t0 + tile * kTile;
@@ -593,10 +612,8 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
         stage_store<VF>(pv, st_v, P.v.pb, vslot, lane);
         wave_sync();
         if (tile + 1 < ntiles) {
-            const int tb2 = tb + kTile;
-            const int n2 = min(kTile, t1 - tb2);
-            prefetch<KF>(P.k, bh * P.k.ts + tb2, n2, lane, pk);
-            prefetch<VF>(P.v, bh * P.v.ts + tb2, n2, lane, pv);
+            prefetch<KF>(wk, P.k.pb, tb + kTile - t0, lane, pk);
+            prefetch<VF>(wv, P.v.pb, tb + kTile - t0, lane, pv);
         }
         // position of this lane's key token (padded tokens reuse the last one)
         const int pos = P.start_pos + tb + min(t, n - 1);
