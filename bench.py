@@ -412,8 +412,8 @@ def measured_traffic(b, t, sparsity, layout):
 def main():
     args = parse()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU; multi-GPU sharding is a design note only "
-                                   "(DESIGN.md), so --gpus above 1 is not supported", "n_gpus": args.gpus}))
+        print(json.dumps({"error": "this build runs on one GPU; multi-GPU sharding is a design note only, "
+                                   "so --gpus above 1 is not supported", "n_gpus": args.gpus}))
         sys.exit(2)
     # keep numpy's CPU baseline single-threaded so `cores` is what was used
     for var in ("OMP_NUM_THREADS", "OPENBLAS_NUM_THREADS", "MKL_NUM_THREADS"):
