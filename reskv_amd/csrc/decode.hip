@@ -12,14 +12,12 @@
 //
 // Partial kernel: one workgroup of 4 waves per (split, kv-head, batch).  A wave
 // walks 16-token tiles of its split.  Each tile's raw bytes (ids, metadata,
-// payload, scales) are copied with 16-byte loads into the wave's LDS stage,
-// prefetching the next tile into registers meanwhile.  Inside a tile the wave
-// works on four tokens at a time: lane L = 16 * row + i takes token 4 * step +
-// row and channels {4i..4i+3} u {64+4i..64+4i+3} (four RoPE pairs), so a score
-// is a 16-lane DPP row sum.  The online softmax runs per tile in the log2
-// domain; the cluster mass beta accumulates with LDS atomics.
-// Merge kernel: one wave per (batch, query head) rescales the split partials to
-// a common maximum, folds sum_c beta_c c_v[c] and normalises.
+// payload, scales) are copied with 16-byte buffer loads into the wave's LDS
+// stage, prefetching the next tile into registers meanwhile; four lanes decode
+// each token (details at the kernel).  Scores, P x V and the cluster mass beta
+// run on the matrix cores; the online softmax runs per tile in the log2 domain.
+// Merge kernel: one workgroup per (batch, query head) rescales the split
+// partials to a common maximum, folds sum_c beta_c c_v[c] and normalises.
 #include "common.h"
 #include "../../include/reskv_hip.h"
 
@@ -43,7 +41,6 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr int kVPitch = kDim + 8;  // halves per token row of the V transpose tile (conflict-free writes)
 constexpr int kCPitch = kDim + 8;  // halves per row of the LDS key-centroid table (staggered banks)
-constexpr int kBetaPitch = kMaxClusters + 1;  // cluster-mass row pitch: the heads of a token hit distinct banks
 
 typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
@@ -80,7 +77,7 @@ struct DParams {
     float qscale;  // scaling * log2(e): scores come out in the log2 domain
     float one;     // 1.0f, opaque to the compiler: fp16 + fp16 sums as one mixed-precision FMA
     int stage_k, stage_v;  // LDS stage bytes per wave for K and V
-    int beta_off, lut_off, p_off, stage_off;  // LDS byte offsets (region 0 holds centroids / merge records)
+    int lut_off, p_off, stage_off;  // LDS byte offsets (region 0 holds centroids / merge records)
     float* pm;
     float* pl;
     float* pd;
@@ -492,8 +489,9 @@ __device__ __forceinline__ float head_sum(float v) {
 // score of token 4((L>>2)&3) + (L>>4) for head (L&3) (+4 for the second set
 // of four heads when G = 8).  The online softmax takes one exponential per
 // lane; the weights, rounded to fp16, drive P x V on v_mfma_f32_4x4x4f16
-// through a per-wave transpose tile, and the cluster mass beta accumulates
-// with LDS atomics.
+// through a per-wave transpose tile, and the cluster mass beta on the same
+// instruction with a one-hot B operand (the tokens' V clusters against
+// cluster `lane`), which keeps it in registers.
 // ---------------------------------------------------------------------------
 template <int G, int KF, int VF, bool TAB>
 __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
@@ -515,7 +513,6 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
     const int t1 = s0 + (int)(((long)(wave + 1) * (s1 - s0)) / kWaves);
 
     uint16_t* s_cent = reinterpret_cast<uint16_t*>(smem);  // region 0: fp16 key centroids [nc][kCPitch]
-    float* my_beta = reinterpret_cast<float*>(smem + P.beta_off) + wave * G * kBetaPitch;
     uint32_t* s_lut = reinterpret_cast<uint32_t*>(smem + P.lut_off);
     // per wave: fp16 weights [4-token group][head][token] and the V tile [token][kVPitch]
     uint16_t* my_p = reinterpret_cast<uint16_t*>(smem + P.p_off) + wave * (kTile * G + kTile * kVPitch);
@@ -534,8 +531,6 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
         const uint4* kc = reinterpret_cast<const uint4*>(P.k.cent + bh * P.k.cs * kDim);
         for (int i = threadIdx.x; i < P.k.nc * (kDim / 8); i += kThreads)
             *reinterpret_cast<uint4*>(s_cent + (i >> 4) * kCPitch + 8 * (i & 15)) = kc[i];
-#pragma unroll
-        for (int g = 0; g < G; ++g) my_beta[g * kBetaPitch + lane] = 0.0f;
     }
 
     // rotated, pre-scaled query values of this lane's channels for heads 4 hs + hj
@@ -583,11 +578,13 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
 
     // P x V sums (v_mfma_f32_4x4x4f16, 16 blocks of 4 lanes): lane L
     // accumulates delta[4 hs + i][L + 64 half] in acc[hs][half][i]
-    float4_t acc[NH][2];
+    // cluster masses on the same matrix cores: B = one-hot of the tokens' V
+    // clusters against cluster `lane`, so lane L accumulates beta[4 hs + i][L] in accb[hs][i]
+    float4_t acc[NH][2], accb[NH];
     float m_run[NH], lv[NH];
 #pragma unroll
     for (int hs = 0; hs < NH; ++hs) {
-        acc[hs][0] = acc[hs][1] = (float4_t){0.0f, 0.0f, 0.0f, 0.0f};
+        acc[hs][0] = acc[hs][1] = accb[hs] = (float4_t){0.0f, 0.0f, 0.0f, 0.0f};
         m_run[hs] = -INFINITY;
         lv[hs] = 0.0f;
     }
@@ -694,13 +691,10 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
                 for (int i = 0; i < 4; ++i) {
                     acc[hs][0][i] *= al[i];
                     acc[hs][1][i] *= al[i];
-                    if constexpr (VT::CENT) {
-                        if (4 * hs + i < G) my_beta[(4 * hs + i) * kBetaPitch + lane] *= al[i];
-                    }
+                    accb[hs][i] *= al[i];
                 }
             }
         }
-        const int vid = VT::CENT ? clamp_id(SV.id(stok), P.v.nc) : 0;
 #pragma unroll
         for (int hs = 0; hs < NH; ++hs) {
             const int g = 4 * hs + hj;
@@ -711,9 +705,6 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
             const float pq = h2f(ph);
             lv[hs] += pq;
             if (g < G) my_p[((((lane >> 2) & 3) * G + g) << 2) + (lane >> 4)] = ph;
-            if constexpr (VT::CENT) {
-                if (ok) atomicAdd(&my_beta[g * kBetaPitch + vid], pq);
-            }
         }
         wave_sync();
 
@@ -729,6 +720,14 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
                     (lds_short4_t*)(vb + 4 * s * kVPitch)));
                 const half4_t b1 = __builtin_bit_cast(half4_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
                     (lds_short4_t*)(vb + 4 * s * kVPitch + 64)));
+                half4_t oh = (half4_t){0, 0, 0, 0};
+                if constexpr (VT::CENT) {
+                    const int4 ids4 = reinterpret_cast<const int4*>(SV.st + kTile * SV.pp + kTile * VT::MB)[s];
+                    const int vids[4] = {ids4.x, ids4.y, ids4.z, ids4.w};
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        oh[r] = clamp_id(vids[r], P.v.nc) == lane ? (_Float16)1.0f : (_Float16)0.0f;
+                }
 #pragma unroll
                 for (int hs = 0; hs < NH; ++hs) {
                     // A: lane 4b + i holds P[head 4 hs + i][tokens 4s + r]
@@ -737,6 +736,7 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
                     if (g < G) a = __builtin_bit_cast(half4_t, *reinterpret_cast<const uint2*>(my_p + ((s * G + g) << 2)));
                     acc[hs][0] = __builtin_amdgcn_mfma_f32_4x4x4f16(a, b0, acc[hs][0], 0, 0, 0);
                     acc[hs][1] = __builtin_amdgcn_mfma_f32_4x4x4f16(a, b1, acc[hs][1], 0, 0, 0);
+                    if constexpr (VT::CENT) accb[hs] = __builtin_amdgcn_mfma_f32_4x4x4f16(a, oh, accb[hs], 0, 0, 0);
                 }
             }
         }
@@ -758,7 +758,7 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
     }
     float bt[G];
 #pragma unroll
-    for (int g = 0; g < G; ++g) bt[g] = KT::CENT ? my_beta[g * kBetaPitch + lane] : 0.0f;
+    for (int g = 0; g < G; ++g) bt[g] = VT::CENT ? accb[g >> 2][g & 3] : 0.0f;
     __syncthreads();  // centroid table and stages no longer needed
     float* rec = reinterpret_cast<float*>(smem) + wave * G * kPartStride;
 #pragma unroll
@@ -1169,8 +1169,7 @@ int run_decode(const void* q, int kf, const DTensor& k, int vf, const DTensor& v
     const int merge_bytes = kWaves * G * kPartStride * 4;
     const int cent_bytes = cent ? k.nc * kCPitch * 2 : 0;
     const int region0 = cent_bytes > merge_bytes ? cent_bytes : merge_bytes;
-    p.beta_off = region0;
-    p.lut_off = p.beta_off + (cent ? (kWaves * G * kBetaPitch * 4 + 15) / 16 * 16 : 0);
+    p.lut_off = region0;
     p.p_off = p.lut_off + kLutWords * 4;
     p.stage_off = p.p_off + kWaves * (kTile * G + kTile * kVPitch) * 2;
     const size_t shm = (size_t)p.stage_off + (size_t)kWaves * (p.stage_k + p.stage_v);
