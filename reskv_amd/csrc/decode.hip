@@ -596,21 +596,30 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
     const int ntiles = (t1 - t0 + kTile - 1) / kTile;
     const WaveSrc<KF> wk = wave_src<KF>(P.k, bh * P.k.ts + t0, t1 - t0);
     const WaveSrc<VF> wv = wave_src<VF>(P.v, bh * P.v.ts + t0, t1 - t0);
-    Prefetch<KF> pk{};
-    Prefetch<VF> pv{};
-    if (ntiles > 0) {
-        prefetch<KF>(wk, P.k.pb, 0, lane, pk);
-        prefetch<VF>(wv, P.v.pb, 0, lane, pv);
+    // Tiles are prefetched kDepth ahead into register buffers used in turn
+    // (two for formats of at most one 16-byte piece per lane and tensor, whose
+    // short tiles would otherwise wait on the load latency; one otherwise).
+    constexpr int kDepth = (KT::PQ + VT::PQ <= 2 && G <= 4) ? 2 : 1;
+    Prefetch<KF> pk[kDepth];
+    Prefetch<VF> pv[kDepth];
+#pragma unroll
+    for (int d = 0; d < kDepth; ++d) {
+        pk[d] = Prefetch<KF>{};
+        pv[d] = Prefetch<VF>{};
+        if (d < ntiles) {
+            prefetch<KF>(wk, P.k.pb, d * kTile, lane, pk[d]);
+            prefetch<VF>(wv, P.v.pb, d * kTile, lane, pv[d]);
+        }
     }
-    for (int tile = 0; tile < ntiles; ++tile) {
+    auto tile_body = [&](int tile, Prefetch<KF>& fk, Prefetch<VF>& fv) {
         const int tb = t0 + tile * kTile;
         const int n = min(kTile, t1 - tb);
-        stage_store<KF>(pk, st_k, P.k.pb, kslot, lane);
-        stage_store<VF>(pv, st_v, P.v.pb, vslot, lane);
+        stage_store<KF>(fk, st_k, P.k.pb, kslot, lane);
+        stage_store<VF>(fv, st_v, P.v.pb, vslot, lane);
         wave_sync();
-        if (tile + 1 < ntiles) {
-            prefetch<KF>(wk, P.k.pb, tb + kTile - t0, lane, pk);
-            prefetch<VF>(wv, P.v.pb, tb + kTile - t0, lane, pv);
+        if (tile + kDepth < ntiles) {
+            prefetch<KF>(wk, P.k.pb, tb + kDepth * kTile - t0, lane, fk);
+            prefetch<VF>(wv, P.v.pb, tb + kDepth * kTile - t0, lane, fv);
         }
         // position of this lane's key token (padded tokens reuse the last one)
         const int pos = P.start_pos + tb + min(t, n - 1);
@@ -647,14 +656,19 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
         float sc[NH];
 #pragma unroll
         for (int hs = 0; hs < NH; ++hs) {
-            float4_t sa = (float4_t){0.0f, 0.0f, 0.0f, 0.0f}, sb = sa;
+            // four independent accumulation chains keep dependent MFMAs apart
+            float4_t sa = (float4_t){0.0f, 0.0f, 0.0f, 0.0f}, sb = sa, sc4 = sa, sd = sa;
 #pragma unroll
-            for (int mi = 0; mi < 32; mi += 2) {
+            for (int mi = 0; mi < 32; mi += 4) {
                 sa = __builtin_amdgcn_mfma_f32_4x4x1f32(x[mi], qv[hs][mi], sa, 0, 0, 0);
                 sb = __builtin_amdgcn_mfma_f32_4x4x1f32(x[mi + 1], qv[hs][mi + 1], sb, 0, 0, 0);
+                sc4 = __builtin_amdgcn_mfma_f32_4x4x1f32(x[mi + 2], qv[hs][mi + 2], sc4, 0, 0, 0);
+                sd = __builtin_amdgcn_mfma_f32_4x4x1f32(x[mi + 3], qv[hs][mi + 3], sd, 0, 0, 0);
             }
-            const float u0 = swap32_sum(sa[0] + sb[0], sa[2] + sb[2]);
-            const float u1 = swap32_sum(sa[1] + sb[1], sa[3] + sb[3]);
+            sa += sb;
+            sc4 += sd;
+            const float u0 = swap32_sum(sa[0] + sc4[0], sa[2] + sc4[2]);
+            const float u1 = swap32_sum(sa[1] + sc4[1], sa[3] + sc4[3]);
             sc[hs] = swap16_sum(u0, u1);
         }
 
@@ -741,6 +755,11 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
             }
         }
         wave_sync();  // stage, tile and weight reads done before the next tile overwrites them
+    };
+    for (int tile = 0; tile < ntiles; tile += kDepth) {
+#pragma unroll
+        for (int d = 0; d < kDepth; ++d)
+            if (tile + d < ntiles) tile_body(tile + d, pk[d], pv[d]);
     }
 
     // ---- per-head totals, then merge the waves through LDS ----
