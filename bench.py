@@ -197,7 +197,7 @@ def measure_encoders(torch, device, reps=20):
     K-means work = 2*T*C*D FLOP per head per iteration for the distances.
     """
     from reskv_amd._extension import load_extension
-    from reskv_amd.compression import cluster
+    from reskv_amd.compression import cluster, cluster_kv
 
     ext = load_extension("compression")
     g = torch.Generator(device=device).manual_seed(1)
@@ -222,9 +222,10 @@ def measure_encoders(torch, device, reps=20):
     vc, vi = cluster(v, 32, 10, value=True)
     us_k = timed(lambda: cluster(k, 32, 10), max(3, reps // 4))
     us_v = timed(lambda: cluster(v, 32, 10, value=True), max(3, reps // 4))
+    us_kv = timed(lambda: cluster_kv(k, v, 32, 10), max(3, reps // 4))
     flop = 2.0 * t * 32 * D * h * 10
-    out["kmeans"] = {"us_k": us_k, "us_v": us_v, "tflops_k": flop / us_k / 1e6, "tflops_v": flop / us_v / 1e6,
-                     "iterations": 10, "clusters": 32}
+    out["kmeans"] = {"us_k": us_k, "us_v": us_v, "us_kv_together": us_kv, "tflops_k": flop / us_k / 1e6,
+                     "tflops_v": flop / us_v / 1e6, "iterations": 10, "clusters": 32}
     n_in = b * h * t * (D * 2 + 4) + b * h * 32 * D * 2
     us = timed(lambda: (ext.compress_fp16(k, kc, ki, 32, True), ext.compress_fp16(v, vc, vi, 32, True)))
     n_out = b * h * t * (32 * 2 + 16)

@@ -84,6 +84,16 @@ int reskv_kmeans(const void* x, const float* centers_init, void* centers_out, in
                  int BH, int T, int C, int iterations, int value_mode, void* workspace,
                  int64_t workspace_bytes, void* stream);
 
+/* A layer's K and V clustered together: the two Lloyd runs of
+ * reskv/compression.py:164-165 (cluster(key), cluster(value, value=True)) as
+ * one sequence of launches over 2*BH problems, K rules for k and V rules for v.
+ * k, v fp16 [BH,T,128]; init_k, init_v fp32 [BH,C,128]; out_k, out_v fp16
+ * [BH,C,128]; ids_k, ids_v int32 [BH,T].  Each result equals the separate
+ * reskv_kmeans call's.  workspace: reskv_kmeans_workspace_bytes(2*BH, T, C). */
+int reskv_kmeans_kv(const void* k, const void* v, const float* init_k, const float* init_v, void* out_k,
+                    void* out_v, int32_t* ids_k, int32_t* ids_v, int BH, int T, int C, int iterations,
+                    void* workspace, int64_t workspace_bytes, void* stream);
+
 /* Assignment step only: ids = argmin_c |x - c|^2 (lowest index on ties).
  * Replaces the assignment of reskv/compression.py:61-69 (_incremental_cluster,
  * one decode group against the shared centroid table).  centers fp32 [BH,C,128];

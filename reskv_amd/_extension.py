@@ -215,6 +215,32 @@ def kmeans(x, centers_init, iterations, value):
     return out, ids
 
 
+def kmeans_kv(k, v, init_k, init_v, iterations):
+    """A layer's K and V clustered in one launch sequence (reskv/compression.py:164-165).
+
+    k, v fp16 [BH, T, 128]; init_k, init_v fp32 [BH, C, 128].  Returns
+    ((centres_k, ids_k), (centres_v, ids_v)), each equal to ``kmeans`` with
+    value=False for K and value=True for V.
+    """
+    for x, c in ((k, init_k), (v, init_v)):
+        _require(x.dtype == torch.float16 and x.dim() == 3 and x.shape[2] == 128, "x must be fp16 [BH,T,128]")
+        _require(c.dtype == torch.float32 and c.dim() == 3, "centres must be fp32 [BH,C,128]")
+    _require(k.shape == v.shape and init_k.shape == init_v.shape and init_k.shape[0] == k.shape[0],
+             "K and V must share [BH, T] and the centroid count")
+    dev = _dev_check(k, v, init_k, init_v)
+    bh, t, _ = k.shape
+    c = init_k.shape[1]
+    outs = [_empty((bh, c, 128), torch.float16, dev) for _ in range(2)]
+    ids = [_empty((bh, t), torch.int32, dev) for _ in range(2)]
+    L = _lib.lib()
+    ws = _workspace(L.reskv_kmeans_workspace_bytes(2 * bh, t, c), dev)
+    with torch.cuda.device(dev):
+        _lib.check(L.reskv_kmeans_kv(k.data_ptr(), v.data_ptr(), init_k.data_ptr(), init_v.data_ptr(),
+                                     outs[0].data_ptr(), outs[1].data_ptr(), ids[0].data_ptr(), ids[1].data_ptr(),
+                                     bh, t, c, int(iterations), ws.data_ptr(), ws.numel(), _stream(dev)), "kmeans_kv")
+    return (outs[0], ids[0]), (outs[1], ids[1])
+
+
 def kmeans_assign(x, centers):
     """Nearest-centre ids, lowest index on ties. x fp16 [BH,T,128]; centres fp32 [BH,C,128]."""
     _require(x.dtype == torch.float16 and x.dim() == 3 and x.shape[2] == 128, "x must be fp16 [BH,T,128]")
@@ -472,7 +498,7 @@ def _make_attention(plan):
 def _make_compression():
     return SimpleNamespace(compress_fp16=compress_fp16, compress_quantized=compress_quantized,
                            compress_structured_int4=compress_structured_int4, compress_bitmap=compress_bitmap,
-                           kmeans=kmeans, kmeans_assign=kmeans_assign)
+                           kmeans=kmeans, kmeans_kv=kmeans_kv, kmeans_assign=kmeans_assign)
 
 
 @lru_cache(maxsize=32)

@@ -3,7 +3,7 @@
 Mirror of ``reskv/compression.py:12-170``: ``cluster``, ``_incremental_cluster``,
 ``_encode`` and ``compress`` keep their names, arguments, validation messages
 and results.  The arithmetic runs in the gfx950 library: Lloyd iterations in
-``reskv_kmeans``, assignment of decode groups in ``reskv_kmeans_assign`` and
+``reskv_kmeans`` (``reskv_kmeans_kv`` for a layer's K and V together), assignment of decode groups in ``reskv_kmeans_assign`` and
 all four residual encoders (including the unstructured FP16 bitmap encoder
 that the reference runs as a chain of PyTorch ops).
 """
@@ -52,6 +52,25 @@ def cluster(x: torch.Tensor, count: int = 32, iterations: int = 10, *, value: bo
     ext = load_extension("compression", device_index=x.device.index or 0)
     centers, ids = ext.kmeans(data.half().contiguous(), init, iterations, value)
     return centers.reshape(b, h, count, d), ids.reshape(b, h, t)
+
+
+def cluster_kv(key: torch.Tensor, value: torch.Tensor, count: int = 32, iterations: int = 10):
+    """``cluster(key, ...)`` and ``cluster(value, ..., value=True)`` as one launch sequence.
+
+    Returns ((k_centres, k_ids), (v_centres, v_ids)), equal to the two separate
+    calls (reskv/compression.py:164-165).  Below ``count`` tokens V caps its
+    centroid count at T, so the two runs have different sizes and run apart.
+    """
+    b, h, t, d = key.shape
+    if t < count:
+        return cluster(key, count, iterations), cluster(value, count, iterations, value=True)
+    kd = key.reshape(b * h, t, d).contiguous()
+    vd = value.reshape(b * h, t, d).contiguous()
+    ik = _initial_centers(kd, count)
+    iv = _initial_centers(vd, count).half().float()  # V centres live in fp16
+    ext = load_extension("compression", device_index=key.device.index or 0)
+    (kc, ki), (vc, vi) = ext.kmeans_kv(kd, vd, ik, iv, iterations)
+    return ((kc.reshape(b, h, count, d), ki.reshape(b, h, t)), (vc.reshape(b, h, count, d), vi.reshape(b, h, t)))
 
 
 def _incremental_cluster(x, centers, config, *, value=False):
@@ -143,8 +162,7 @@ def compress(
         k, v = _compress_group(key, value, config, previous, plan)
         return CompressedKV(previous.key.append(k), previous.value.append(v))
     else:
-        kc, ki = cluster(key, config.num_clusters, config.kmeans_iterations)
-        vc, vi = cluster(value, config.num_clusters, config.kmeans_iterations, value=True)
+        (kc, ki), (vc, vi) = cluster_kv(key, value, config.num_clusters, config.kmeans_iterations)
     k = _encode(key, kc, ki, plan)
     v = _encode(value, vc, vi, plan, value=True)
     return CompressedKV(k, v)

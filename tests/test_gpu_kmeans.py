@@ -9,7 +9,7 @@ import pytest
 import torch
 
 from oracle import reskv_oracle as o
-from reskv_amd.compression import _incremental_cluster, cluster
+from reskv_amd.compression import _incremental_cluster, cluster, cluster_kv
 from reskv_amd import ResKVKernelConfig
 from tests.gpu_helpers import np_, outlier_kv, seeded
 
@@ -96,3 +96,14 @@ def test_incremental_cluster_matches_oracle(device):
     _tie_free_equal(np_(ids).reshape(4, -1), eids.reshape(4, -1), margin, data, cen)
     c3, _ = _incremental_cluster(x, c2, cfg)  # at the cap: no new centre
     assert c3.shape[2] == 21
+
+
+@pytest.mark.parametrize("t,count", [(1000, 32), (300, 20), (2100, 64), (40, 8)])
+def test_paired_kv_clustering_equals_separate_runs(device, t, count):
+    """K and V in one launch sequence give exactly the two separate runs' results."""
+    k, v, _ = outlier_kv(2, 3, t, seed=31)
+    (kc, ki), (vc, vi) = cluster_kv(k, v, count, 5)
+    ek, eki = cluster(k, count, 5)
+    ev, evi = cluster(v, count, 5, value=True)
+    assert torch.equal(ki, eki) and torch.equal(vi, evi)
+    assert torch.equal(kc, ek) and torch.equal(vc, ev)
