@@ -111,6 +111,100 @@ __global__ void __launch_bounds__(256) encode_qtile_kernel(
     }
 }
 
+// ---------------------------------------------------------------------------
+// 4 of 16 per tile (structured 4:16 at 75%): eight lanes per token, lane
+// 8 t + j owns 16-channel tile j of token t, so a wave encodes 8 tokens and
+// every load and store is a contiguous run of the token's row.
+//
+// fp16(f32(x) - f32(c)) equals the correctly rounded fp16 difference for every
+// pair of finite fp16 values (checked exhaustively), so residuals come from
+// packed fp16 subtraction.  Each channel j of the tile gets the unique key
+//   (|h| << 5) | ((15 - j) << 1) | sign(h)
+// (magnitude first, lower channel on ties, the fp16 bits recoverable from the
+// key); a selection network yields the top 4 keys, which are then put in
+// channel order.
+// ---------------------------------------------------------------------------
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef short short2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ void cx_desc(uint32_t& a, uint32_t& b) {  // a >= b afterwards
+    const uint32_t hi = max(a, b), lo = min(a, b);
+    a = hi;
+    b = lo;
+}
+__device__ __forceinline__ void sort4_desc(uint32_t& a, uint32_t& b, uint32_t& c, uint32_t& d) {
+    cx_desc(a, b);
+    cx_desc(c, d);
+    cx_desc(a, c);
+    cx_desc(b, d);
+    cx_desc(b, c);
+}
+// a, b: descending lists of 4.  a becomes the descending top 4 of both:
+// max(a_i, b_{3-i}) is that set as a bitonic sequence, then a half-cleaner
+// merge sorts it.
+__device__ __forceinline__ void merge_top4(uint32_t* a, const uint32_t* b) {
+    uint32_t c0 = max(a[0], b[3]), c1 = max(a[1], b[2]), c2 = max(a[2], b[1]), c3 = max(a[3], b[0]);
+    cx_desc(c0, c2);
+    cx_desc(c1, c3);
+    cx_desc(c0, c1);
+    cx_desc(c2, c3);
+    a[0] = c0;
+    a[1] = c1;
+    a[2] = c2;
+    a[3] = c3;
+}
+
+__global__ void __launch_bounds__(256) encode_tile4_kernel(
+    const uint16_t* __restrict__ keys, const uint16_t* __restrict__ cent,
+    const int32_t* __restrict__ ids, uint16_t* __restrict__ payload, int32_t* __restrict__ meta,
+    long rows, int T, int C, int struct_index) {
+    const int lane = threadIdx.x & 63;
+    const long row = ((long)blockIdx.x * 4 + (threadIdx.x >> 6)) * 8 + (lane >> 3);
+    const int tile = lane & 7;
+    if (row >= rows) return;
+    const long bh = row / T;
+    int cid = ids[row];
+    cid = cid < 0 ? 0 : (cid > C - 1 ? C - 1 : cid);  // compression.cu:83-84
+    const uint4* xp = reinterpret_cast<const uint4*>(keys + row * kDim + tile * 16);
+    const uint4* cp = reinterpret_cast<const uint4*>(cent + (bh * C + cid) * kDim + tile * 16);
+    const uint4 xa = xp[0], xb = xp[1], ca = cp[0], cb = cp[1];
+    const uint32_t xw[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+    const uint32_t cw[8] = {ca.x, ca.y, ca.z, ca.w, cb.x, cb.y, cb.z, cb.w};
+    uint32_t k[16];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const uint32_t h = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, xw[i]) - __builtin_bit_cast(half2_t, cw[i]));
+        const uint32_t lo = h & 0xFFFFu, hi = h >> 16;
+        k[2 * i] = ((lo & 0x7FFFu) << 5) | ((uint32_t)(15 - 2 * i) << 1) | (lo >> 15);
+        k[2 * i + 1] = ((hi & 0x7FFFu) << 5) | ((uint32_t)(14 - 2 * i) << 1) | (hi >> 15);
+    }
+#pragma unroll
+    for (int g = 0; g < 4; ++g) sort4_desc(k[4 * g], k[4 * g + 1], k[4 * g + 2], k[4 * g + 3]);
+    merge_top4(k, k + 4);
+    merge_top4(k + 8, k + 12);
+    // the top 4 of all 16 (unordered), re-keyed by channel: (15 - j) << 16 | fp16 bits
+    uint32_t s[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t t = max(k[i], k[11 - i]);
+        s[i] = ((t & 0x1Eu) << 15) | ((t & 1u) << 15) | (t >> 5);
+    }
+    sort4_desc(s[0], s[1], s[2], s[3]);  // ascending channel
+    uint2 pw;
+    pw.x = (s[0] & 0xFFFFu) | (s[1] << 16);
+    pw.y = (s[2] & 0xFFFFu) | (s[3] << 16);
+    *reinterpret_cast<uint2*>(payload + row * 32 + tile * 4) = pw;
+    uint32_t code = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t j = 15u - (s[i] >> 16);
+        code |= struct_index ? j << (4 * i) : 1u << j;
+    }
+    // word w = code(tile 2w) | code(tile 2w+1) << 16
+    const uint32_t other = dpp_u<0xB1>(code);  // quad xor 1: the neighbouring tile
+    if ((tile & 1) == 0) meta[row * 4 + (tile >> 1)] = (int32_t)(code | (other << 16));
+}
+
 __global__ void __launch_bounds__(256) encode_bitmap_kernel(
     const uint16_t* __restrict__ keys, const uint16_t* __restrict__ cent,
     const int32_t* __restrict__ ids, uint16_t* __restrict__ payload, int64_t* __restrict__ meta,
@@ -130,6 +224,108 @@ __global__ void __launch_bounds__(256) encode_bitmap_kernel(
         // channel d -> bit (63 - d % 64) of word d / 64 (compression.py:87-88)
         if (lane < 2) meta[row * 2 + lane] = (int64_t)bitrev64(lane == 0 ? b0 : b1);
     }
+}
+
+// ---------------------------------------------------------------------------
+// Unstructured top-nnz with MSB-first bitmaps, eight lanes per token (lane
+// 8 t + j owns channels 16 j .. 16 j + 15 of token t).  The nnz-th largest
+// magnitude M comes from a 15-step search over the fp16 magnitude bits; each
+// step counts the token's magnitudes below the candidate with packed 16-bit
+// subtractions (sign bits gathered into one popcount) and three lane sums.
+// Channels above M are kept, and the lowest-indexed channels equal to M fill
+// the remainder (ties go to the lower channel, as with the composite key).
+// ---------------------------------------------------------------------------
+// Number of the lane's 16 magnitudes (packed pairs mp) below cand.
+__device__ __forceinline__ int count_below(const uint32_t* mp, uint32_t cand) {
+    const uint32_t cc = cand | (cand << 16);
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        // sign bit of each 16-bit difference: set where the magnitude is below cand
+        const uint32_t d0 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(short2_t, mp[2 * i]) - __builtin_bit_cast(short2_t, cc));
+        const uint32_t d1 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(short2_t, mp[2 * i + 1]) - __builtin_bit_cast(short2_t, cc));
+        w[i] = __builtin_amdgcn_perm(d1, d0, 0x07050301u);  // the four high bytes
+    }
+    const uint32_t g = (w[0] & 0x80808080u) | ((w[1] >> 1) & 0x40404040u) | ((w[2] >> 2) & 0x20202020u) |
+                       ((w[3] >> 3) & 0x10101010u);
+    return __builtin_popcount(g);
+}
+// Sum over the 8 lanes of the lane's token (lanes 8t .. 8t+7), in every one of them.
+__device__ __forceinline__ int token_sum8(int v) {
+    v += (int)dpp_u<0xB1>((uint32_t)v);   // quad xor 1
+    v += (int)dpp_u<0x4E>((uint32_t)v);   // quad xor 2
+    v += (int)dpp_u<0x141>((uint32_t)v);  // half-row mirror: the other quad of the 8
+    return v;
+}
+// Exclusive prefix sum over the lanes of the token, in channel order.
+__device__ __forceinline__ int token_prefix8(int v, int j) {
+    int x = v;
+#pragma unroll
+    for (int sh = 1; sh < 8; sh <<= 1) {
+        const int o = __shfl_up(x, sh, 8);
+        x += j >= sh ? o : 0;
+    }
+    return x - v;
+}
+
+__global__ void __launch_bounds__(256) encode_bitmap8_kernel(
+    const uint16_t* __restrict__ keys, const uint16_t* __restrict__ cent,
+    const int32_t* __restrict__ ids, uint16_t* __restrict__ payload, int64_t* __restrict__ meta,
+    long rows, int T, int C, int nnz) {
+    const int lane = threadIdx.x & 63;
+    const long row = ((long)blockIdx.x * 4 + (threadIdx.x >> 6)) * 8 + (lane >> 3);
+    const int tile = lane & 7;
+    if (row >= rows) return;
+    const long bh = row / T;
+    int cid = ids[row];
+    cid = cid < 0 ? 0 : (cid > C - 1 ? C - 1 : cid);  // compression.cu:83-84
+    const uint4* xp = reinterpret_cast<const uint4*>(keys + row * kDim + tile * 16);
+    const uint4* cp = reinterpret_cast<const uint4*>(cent + (bh * C + cid) * kDim + tile * 16);
+    const uint4 xa = xp[0], xb = xp[1], ca = cp[0], cb = cp[1];
+    const uint32_t xw[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+    const uint32_t cw[8] = {ca.x, ca.y, ca.z, ca.w, cb.x, cb.y, cb.z, cb.w};
+    uint32_t hp[8], mp[8];  // fp16 residual pairs, their magnitudes
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        hp[i] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, xw[i]) - __builtin_bit_cast(half2_t, cw[i]));
+        mp[i] = hp[i] & 0x7FFF7FFFu;
+    }
+    // M = the largest magnitude with at least nnz of the token's magnitudes >= M
+    uint32_t m = 0;
+#pragma unroll 1
+    for (int bit = 14; bit >= 0; --bit) {
+        const uint32_t cand = m | (1u << bit);
+        const int ge = kDim - token_sum8(count_below(mp, cand));
+        m = ge >= nnz ? cand : m;
+    }
+    // channels above M, channels equal to M
+    uint32_t gt = 0, eq = 0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const uint32_t v = (mp[i >> 1] >> (16 * (i & 1))) & 0xFFFFu;
+        gt |= (v > m ? 1u : 0u) << i;
+        eq |= (v == m ? 1u : 0u) << i;
+    }
+    const int need = nnz - token_sum8(__builtin_popcount(gt));  // ties to take, lowest channels first
+    int quota = need - token_prefix8(__builtin_popcount(eq), tile);
+    quota = quota < 0 ? 0 : quota;
+    while (__builtin_popcount(eq) > quota) eq &= ~(0x80000000u >> __builtin_clz(eq));  // drop the highest tie
+    const uint32_t sel = gt | eq;
+    // payload: the token's kept residuals in channel order
+    uint16_t* prow = payload + row * nnz + token_prefix8(__builtin_popcount(sel), tile);
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+        if ((sel >> i) & 1u) prow[__builtin_popcount(sel & ((1u << i) - 1u))] = (uint16_t)(hp[i >> 1] >> (16 * (i & 1)));
+    // channel d -> bit (63 - d % 64) of word d / 64 (compression.py:87-88)
+    const uint32_t rev = __builtin_bitreverse32(sel) >> 16;  // channel 16 tile + i -> bit 15 - i
+    uint32_t lo = (tile & 1) ? rev : rev << 16, hi = lo;     // 32-bit halves of the tile pair
+    lo = (tile & 2) ? lo : 0u;
+    hi = (tile & 2) ? 0u : hi;
+    lo |= dpp_u<0xB1>(lo);
+    hi |= dpp_u<0xB1>(hi);
+    lo |= dpp_u<0x4E>(lo);
+    hi |= dpp_u<0x4E>(hi);
+    if ((tile & 3) == 0) meta[row * 2 + (tile >> 2)] = (int64_t)(((uint64_t)hi << 32) | lo);
 }
 
 template <int BITS>
@@ -252,6 +448,12 @@ extern "C" int reskv_compress_fp16(const void* keys, const void* centroids, cons
                   "FP16 tile encoder requires nnz divisible by 8 and < 128");
     RESKV_REQUIRE(!struct_index || nnz == 32, "4:16 index codes require nnz == 32");
     const long rows = (long)B * H * T;
+    if (nnz == 32 && (((uintptr_t)keys | (uintptr_t)centroids) & 15u) == 0 && ((uintptr_t)payload & 7u) == 0) {
+        hipLaunchKernelGGL(encode_tile4_kernel, dim3((int)((rows + 31) / 32)), dim3(256), 0, (hipStream_t)stream,
+                           (const uint16_t*)keys, (const uint16_t*)centroids, ids, (uint16_t*)payload, meta, rows, T,
+                           C, struct_index);
+        return reskv_host::check_launch("encode_tile4_kernel");
+    }
     hipLaunchKernelGGL(encode_qtile_kernel, dim3(grid_for(rows)), dim3(256), 0, (hipStream_t)stream,
                        (const uint16_t*)keys, (const uint16_t*)centroids, ids, (uint16_t*)payload, meta,
                        rows, T, C, nnz, struct_index);
@@ -265,6 +467,12 @@ extern "C" int reskv_compress_bitmap(const void* keys, const void* centroids, co
     RESKV_REQUIRE(payload && meta, "null output pointer");
     RESKV_REQUIRE(nnz > 0 && nnz <= kDim, "nnz must be in [1, 128]");
     const long rows = (long)B * H * T;
+    if ((((uintptr_t)keys | (uintptr_t)centroids) & 15u) == 0) {
+        hipLaunchKernelGGL(encode_bitmap8_kernel, dim3((int)((rows + 31) / 32)), dim3(256), 0, (hipStream_t)stream,
+                           (const uint16_t*)keys, (const uint16_t*)centroids, ids, (uint16_t*)payload, meta, rows, T,
+                           C, nnz);
+        return reskv_host::check_launch("encode_bitmap8_kernel");
+    }
     hipLaunchKernelGGL(encode_bitmap_kernel, dim3(grid_for(rows)), dim3(256), 0, (hipStream_t)stream,
                        (const uint16_t*)keys, (const uint16_t*)centroids, ids, (uint16_t*)payload, meta,
                        rows, T, C, nnz);

@@ -41,7 +41,7 @@ def ext(device):
 
 
 @pytest.mark.parametrize("kind", KINDS)
-@pytest.mark.parametrize("nnz", [64, 32])
+@pytest.mark.parametrize("nnz", [64, 32, 1, 127, 128])
 def test_bitmap_encoder(ext, device, kind, nnz):
     x, c, ids = _case(kind, 2, 3, 77, 5, 1, device)
     payload, meta = ext.compress_bitmap(x, c, ids, nnz)
