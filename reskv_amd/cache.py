@@ -14,12 +14,17 @@ The compressed history lives in device buffers with preallocated capacity,
 instead of being re-concatenated (``torch.cat``) at every group. Capacity
 doubles when it runs out. ``compressed`` is a ``CompressedKV`` of views into
 those buffers; the decode kernels read the views in place through their row
-strides. The transformers ``Cache`` base classes are not required: the layer
-and cache objects expose the same methods duck-typed, so the cache works with
-the model patch and without a particular transformers version.
+strides. When transformers is importable the classes derive from its
+``CacheLayerMixin`` / ``Cache`` (as the reference's do), so ``generate`` and the
+mask builders accept them; without it they are the same methods duck-typed.
 """
 
 import torch
+
+try:
+    from transformers.cache_utils import Cache as _CacheBase, CacheLayerMixin as _LayerBase
+except ImportError:  # the kernels and the harness do not need transformers
+    _CacheBase = _LayerBase = object
 
 from ._extension import StepDecoder
 from .compression import _compress_group, compress
@@ -99,10 +104,11 @@ class _Store:
                 setattr(self, name, buf.index_select(0, index.to(buf.device)))
 
 
-class ResKVLayerCache:
+class ResKVLayerCache(_LayerBase):
     """One layer's cache (reskv/cache.py:11-103)."""
 
     is_sliding = False
+    is_compileable = False
 
     def __init__(self, config: ResKVKernelConfig, capacity: int | None = None):
         self.config = config
@@ -215,6 +221,9 @@ class ResKVLayerCache:
     def get_max_cache_shape(self):
         return -1
 
+    def get_max_length(self):
+        return -1
+
     def reset(self):
         self.keys = self.values = self.raw_keys = None
         self._k = self._v = self._view = None
@@ -235,12 +244,16 @@ class ResKVLayerCache:
                 self._view = None
 
 
-class ResKVCache:
+class ResKVCache(_CacheBase):
     """Per-layer ResKV caches for a decoder stack (reskv/cache.py:106-122)."""
 
     def __init__(self, config: ResKVKernelConfig, num_layers: int, capacity: int | None = None):
+        layers = [ResKVLayerCache(config, capacity) for _ in range(num_layers)]
+        if _CacheBase is object:
+            self.layers = layers
+        else:
+            super().__init__(layers=layers)
         self.config = config
-        self.layers = [ResKVLayerCache(config, capacity) for _ in range(num_layers)]
 
     def __len__(self):
         return len(self.layers)
@@ -250,6 +263,9 @@ class ResKVCache:
 
     def get_seq_length(self, layer_idx=0):
         return self.layers[layer_idx].get_seq_length()
+
+    def get_mask_sizes(self, query_length, layer_idx=0):
+        return self.layers[layer_idx].get_mask_sizes(query_length)
 
     def crop(self, max_length):
         raise NotImplementedError("ResKV does not support speculative cache rollback")

@@ -1,0 +1,83 @@
+"""Model patch (reskv/models/llama.py) on CPU: before the first group is
+compressed every step attends densely, so greedy decoding must equal the stock
+transformers Llama with the same weights; plus the constructor and forward
+checks of the reference."""
+
+import pytest
+import torch
+
+transformers = pytest.importorskip("transformers")
+from transformers import LlamaConfig, LlamaForCausalLM  # noqa: E402
+
+from reskv_amd import ResKVForCausalLM, ResKVKernelConfig  # noqa: E402
+from reskv_amd.cache import ResKVCache  # noqa: E402
+
+
+def _config(**kw):
+    base = dict(vocab_size=300, hidden_size=512, intermediate_size=768, num_hidden_layers=2, num_attention_heads=4,
+                num_key_value_heads=1, max_position_embeddings=2048)
+    base.update(kw)
+    return LlamaConfig(**base)
+
+
+def test_uncompressed_decode_equals_stock_llama():
+    torch.manual_seed(0)
+    stock = LlamaForCausalLM(_config()).eval()
+    model = ResKVForCausalLM(_config(), ResKVKernelConfig()).eval()
+    model.load_state_dict(stock.state_dict())
+    ids = torch.randint(5, 300, (2, 24), generator=torch.Generator().manual_seed(1))
+    mask = torch.ones_like(ids)
+    with torch.no_grad():
+        want = stock.generate(ids, attention_mask=mask, max_new_tokens=40, do_sample=False, pad_token_id=0)
+        got = model.generate(ids, attention_mask=mask, max_new_tokens=40, do_sample=False, pad_token_id=0)
+    assert torch.equal(got, want)  # 24 + 40 tokens stay inside the 96-slot ring
+
+
+def test_forward_returns_a_resKV_cache_and_counts_tokens():
+    model = ResKVForCausalLM(_config(), ResKVKernelConfig()).eval()
+    ids = torch.randint(5, 300, (1, 10))
+    with torch.no_grad():
+        out = model(ids)
+        cache = out.past_key_values
+        assert isinstance(cache, ResKVCache) and cache.get_seq_length() == 10
+        out = model(ids[:, :1], past_key_values=cache)
+    assert cache.get_seq_length() == 11 and all(layer.live == 11 for layer in cache.layers)
+    assert out.logits.shape == (1, 1, 300)
+
+
+def test_settings_are_stored_in_the_model_config():
+    cfg = _config()
+    model = ResKVForCausalLM(cfg, ResKVKernelConfig(sparsity=0.75, num_clusters=16))
+    assert cfg.reskv_kernel_config["sparsity"] == 0.75 and model.kernel_config.num_clusters == 16
+    again = ResKVForCausalLM(cfg)  # read back from the config
+    assert again.kernel_config == model.kernel_config
+
+
+@pytest.mark.parametrize("kw,match", [
+    (dict(hidden_size=256, num_attention_heads=4, num_key_value_heads=1), "head_dim"),
+    (dict(num_attention_heads=4, num_key_value_heads=2), "GQA"),
+    (dict(num_attention_heads=4, num_key_value_heads=3), "multiple"),
+])
+def test_unsupported_shapes_rejected(kw, match):
+    with pytest.raises(ValueError, match=match):
+        ResKVForCausalLM(_config(**kw))
+
+
+def test_forward_checks():
+    model = ResKVForCausalLM(_config(), ResKVKernelConfig())
+    ids = torch.randint(5, 300, (2, 6))
+    with pytest.raises(ValueError, match="eval"):
+        model(ids)  # training mode
+    model.eval()
+    with torch.no_grad():
+        with pytest.raises(ValueError, match="unpadded"):
+            model(ids, attention_mask=torch.tensor([[1] * 6, [0] + [1] * 5]))
+        with pytest.raises(ValueError, match="ResKVCache"):
+            model(ids, past_key_values=object())
+        with pytest.raises(ValueError, match="contiguous"):
+            model(ids, position_ids=torch.arange(1, 7)[None])
+        with pytest.raises(ValueError, match="exactly one"):
+            model()
+        cache = model(ids).past_key_values
+        with pytest.raises(ValueError, match="single-token"):
+            model(ids[:, :2], past_key_values=cache)
