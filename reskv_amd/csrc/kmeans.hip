@@ -46,6 +46,7 @@ constexpr int kRegions = 4;  // LDS sum regions: waves w and w + 4 share region 
 constexpr int kThreads = kWaves * kWave;
 constexpr int kSub = 16;           // tokens per MFMA sub-tile
 constexpr int kChunk = 256;        // tokens per assignment workgroup (two sub-tiles per wave)
+constexpr int kCUs = 256;          // compute units of an MI355X
 constexpr int kXPitch = kDim + 8;  // halves per staged token row (16-byte aligned rows)
 constexpr int kRPitch = kDim + 4;  // floats per cluster row of a wave's sum region; column kDim is the count
 
@@ -123,14 +124,16 @@ __global__ void __launch_bounds__(kDim) kmeans_prep_kernel(const float* __restri
 // thi/tlo fp16 [BH, 16 NB, 128] and tnorm fp32 [BH, 16 NB] are the centre
 // tables; psum fp32 [BH, chunks, C, 128] and pcnt int [BH, chunks, C] (skipped
 // when psum is null).  LO: some problem has fp32 centres (lo tables of the
-// others are zero).
-template <int NB, bool LO>
+// others are zero).  REGB: centre operands held in registers (one workgroup per
+// CU); otherwise read from LDS, which halves the registers so that two
+// workgroups share a CU when the grid has more workgroups than CUs.
+template <int NB, bool LO, bool REGB>
 __global__ void __launch_bounds__(kThreads) kmeans_assign_kernel(
     Problems P, const uint16_t* __restrict__ thi, const uint16_t* __restrict__ tlo, const float* __restrict__ tnorm,
     float* __restrict__ psum, int* __restrict__ pcnt, int T, int C, int chunks) {
     constexpr int CP = NB * 16;
     constexpr int SPW = kChunk / (kWaves * kSub);  // sub-tiles per wave
-    constexpr bool kRegB = NB <= 2;  // centre operands in registers; larger tables go through LDS
+    constexpr bool kRegB = REGB && NB <= 2;
     __shared__ __align__(16) unsigned char smem[smem_bytes<NB>()];
     const int chunk = blockIdx.x;
     const long bh = blockIdx.y;
@@ -409,26 +412,33 @@ struct Tables {
     float* norm;
 };
 
-template <int NB>
+template <int NB, bool REGB>
 void launch_nb(bool lo, dim3 grid, hipStream_t st, const Problems& P, const Tables& tb, float* psum, int* pcnt, int T,
                int C, int chunks) {
     if (lo)
-        hipLaunchKernelGGL((kmeans_assign_kernel<NB, true>), grid, dim3(kThreads), 0, st, P, tb.hi, tb.lo, tb.norm,
-                           psum, pcnt, T, C, chunks);
+        hipLaunchKernelGGL((kmeans_assign_kernel<NB, true, REGB>), grid, dim3(kThreads), 0, st, P, tb.hi, tb.lo,
+                           tb.norm, psum, pcnt, T, C, chunks);
     else
-        hipLaunchKernelGGL((kmeans_assign_kernel<NB, false>), grid, dim3(kThreads), 0, st, P, tb.hi, tb.lo, tb.norm,
-                           psum, pcnt, T, C, chunks);
+        hipLaunchKernelGGL((kmeans_assign_kernel<NB, false, REGB>), grid, dim3(kThreads), 0, st, P, tb.hi, tb.lo,
+                           tb.norm, psum, pcnt, T, C, chunks);
 }
 
 int launch_assign(const Problems& P, const Tables& tb, float* psum, int* pcnt, int BH, int T, int C, const Layout& L,
                   hipStream_t st) {
     const dim3 grid(L.chunks, BH);
     const bool lo = P.vfrom > 0;
+    const bool regb = (int64_t)L.chunks * BH <= kCUs;  // one workgroup per CU: registers; more: LDS operands
     switch (L.Cp / 16) {
-    case 1: launch_nb<1>(lo, grid, st, P, tb, psum, pcnt, T, C, L.chunks); break;
-    case 2: launch_nb<2>(lo, grid, st, P, tb, psum, pcnt, T, C, L.chunks); break;
-    case 3: launch_nb<3>(lo, grid, st, P, tb, psum, pcnt, T, C, L.chunks); break;
-    default: launch_nb<4>(lo, grid, st, P, tb, psum, pcnt, T, C, L.chunks); break;
+    case 1:
+        if (regb) launch_nb<1, true>(lo, grid, st, P, tb, psum, pcnt, T, C, L.chunks);
+        else launch_nb<1, false>(lo, grid, st, P, tb, psum, pcnt, T, C, L.chunks);
+        break;
+    case 2:
+        if (regb) launch_nb<2, true>(lo, grid, st, P, tb, psum, pcnt, T, C, L.chunks);
+        else launch_nb<2, false>(lo, grid, st, P, tb, psum, pcnt, T, C, L.chunks);
+        break;
+    case 3: launch_nb<3, false>(lo, grid, st, P, tb, psum, pcnt, T, C, L.chunks); break;
+    default: launch_nb<4, false>(lo, grid, st, P, tb, psum, pcnt, T, C, L.chunks); break;
     }
     return reskv_host::check_launch("kmeans_assign_kernel");
 }

@@ -107,3 +107,14 @@ def test_paired_kv_clustering_equals_separate_runs(device, t, count):
     ev, evi = cluster(v, count, 5, value=True)
     assert torch.equal(ki, eki) and torch.equal(vi, evi)
     assert torch.equal(kc, ek) and torch.equal(vc, ev)
+
+
+def test_paired_kv_clustering_at_config1_scale(device):
+    """Config 1 shape: the separate runs (256 workgroups, centre operands in
+    registers) and the paired run (512 workgroups, operands from LDS) agree exactly."""
+    k, v, _ = outlier_kv(1, 8, 8192, seed=41)
+    (kc, ki), (vc, vi) = cluster_kv(k, v, 32, 3)
+    ek, eki = cluster(k, 32, 3)
+    ev, evi = cluster(v, 32, 3, value=True)
+    assert torch.equal(ki, eki) and torch.equal(vi, evi)
+    assert torch.equal(kc, ek) and torch.equal(vc, ev)
