@@ -426,6 +426,13 @@ def main():
         sys.exit(1)
     device = "cuda:0"
     torch.cuda.set_device(0)
+    if args.calibrate_copy:
+        src = torch.empty(256 << 20, dtype=torch.uint8, device=device).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     if args.only == "encode":
         print(json.dumps({"encode": measure_encoders(torch, device)}), flush=True)
         return
@@ -436,13 +443,6 @@ def main():
         print(json.dumps({"e2e": measure_e2e(torch, device, args.e2e_batch, args.e2e_prompt, args.e2e_steps)}),
               flush=True)
         return
-    if args.calibrate_copy:
-        src = torch.empty(256 << 20, dtype=torch.uint8, device=device).fill_(1)
-        dst = torch.empty_like(src)
-        for _ in range(3):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        del src, dst
     r = measure_point(torch, args.batch, args.seq_len, args.sparsity, args.layout, args.layers, args.steps,
                       args.warmup, args.splits, device, eager=True)
     print(json.dumps({"point": r}), flush=True)
