@@ -164,11 +164,13 @@ __device__ __forceinline__ void prefetch(const WaveSrc<F>& W, int pb, int off, i
 }
 
 // Stage layout (bytes): payload [16][pb + 16] | meta [16][MB] | ids int32[16] |
-// scale f32[16].  The 16-byte pad staggers consecutive payload rows over the
-// LDS banks (16 lanes read 16 different rows at similar offsets).
+// scale f32[16] | ids uint8[16].  Ids are stored clamped to [0, nc - 1]; the
+// byte copy feeds the one-hot operand of the cluster mass.  The 16-byte pad
+// staggers consecutive payload rows over the LDS banks (16 lanes read 16
+// different rows at similar offsets).
 template <int F>
 __host__ __device__ constexpr int stage_bytes(int pb) {
-    return kTile * (pb + 16) + kTile * Traits<F>::MB + 2 * kTile * 4;
+    return kTile * (pb + 16) + kTile * Traits<F>::MB + 2 * kTile * 4 + kTile;
 }
 
 // LDS byte offsets of this lane's prefetch pieces inside the stage (piece
@@ -185,7 +187,8 @@ __device__ __forceinline__ void stage_slots(int pb, int lane, int* slot) {
 }
 
 template <int F>
-__device__ __forceinline__ void stage_store(const Prefetch<F>& P, uint8_t* st, int pb, const int* slot, int lane) {
+__device__ __forceinline__ void stage_store(const Prefetch<F>& P, uint8_t* st, int pb, const int* slot, int lane,
+                                            int nc) {
     using Tr = Traits<F>;
 #pragma unroll
     for (int i = 0; i < Tr::PQ; ++i)
@@ -195,8 +198,10 @@ __device__ __forceinline__ void stage_store(const Prefetch<F>& P, uint8_t* st, i
         if constexpr (Tr::MB == 16) reinterpret_cast<uint4*>(meta)[lane] = P.meta;
         if constexpr (Tr::MB == 8) reinterpret_cast<uint2*>(meta)[lane] = make_uint2(P.meta.x, P.meta.y);
         int* ids = reinterpret_cast<int*>(meta + kTile * Tr::MB);
-        ids[lane] = P.id;
+        const int cid = P.id < 0 ? 0 : (P.id >= nc ? nc - 1 : P.id);  // compression.cu:83-84
+        ids[lane] = cid;
         reinterpret_cast<float*>(ids + kTile)[lane] = P.sc;
+        reinterpret_cast<uint8_t*>(ids + 2 * kTile)[lane] = (uint8_t)cid;
     }
 }
 
@@ -211,6 +216,9 @@ struct StageView {
     }
     __device__ float scale(int t) const {
         return reinterpret_cast<const float*>(st + kTile * pp + kTile * Traits<F>::MB + kTile * 4)[t];
+    }
+    __device__ uint32_t ids4(int s) const {  // clamped ids of tokens 4s .. 4s+3, one byte each
+        return reinterpret_cast<const uint32_t*>(st + kTile * pp + kTile * Traits<F>::MB + 2 * kTile * 4)[s];
     }
 };
 
@@ -403,7 +411,7 @@ __device__ __forceinline__ void key_values(const StageView<F>& S, int t, int g, 
                                            const uint32_t* lut, const uint16_t* s_cent, int nc, float one, float* x) {
     uint32_t c[16];
     if constexpr (Traits<F>::CENT) {
-        const int kid = clamp_id(S.id(t), nc);
+        const int kid = S.id(t);  // clamped when staged
         const uint4* cr = reinterpret_cast<const uint4*>(s_cent + kid * kCPitch);
         const uint4 a = cr[2 * g], b = cr[2 * g + 1], d = cr[8 + 2 * g], e = cr[9 + 2 * g];
         const uint32_t v[16] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w, d.x, d.y, d.z, d.w, e.x, e.y, e.z, e.w};
@@ -589,6 +597,7 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
         lv[hs] = 0.0f;
     }
     int kslot[KT::PQ], vslot[VT::PQ];
+    const uint32_t lane_bytes = (uint32_t)lane * 0x01010101u;
     stage_slots<KF>(P.k.pb, lane, kslot);
     stage_slots<VF>(P.v.pb, lane, vslot);
     __syncthreads();
@@ -614,8 +623,8 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
     auto tile_body = [&](int tile, Prefetch<KF>& fk, Prefetch<VF>& fv) {
         const int tb = t0 + tile * kTile;
         const int n = min(kTile, t1 - tb);
-        stage_store<KF>(fk, st_k, P.k.pb, kslot, lane);
-        stage_store<VF>(fv, st_v, P.v.pb, vslot, lane);
+        stage_store<KF>(fk, st_k, P.k.pb, kslot, lane, P.k.nc);
+        stage_store<VF>(fv, st_v, P.v.pb, vslot, lane, P.v.nc);
         wave_sync();
         if (tile + kDepth < ntiles) {
             prefetch<KF>(wk, P.k.pb, tb + kDepth * kTile - t0, lane, fk);
@@ -736,11 +745,14 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
                     (lds_short4_t*)(vb + 4 * s * kVPitch + 64)));
                 half4_t oh = (half4_t){0, 0, 0, 0};
                 if constexpr (VT::CENT) {
-                    const int4 ids4 = reinterpret_cast<const int4*>(SV.st + kTile * SV.pp + kTile * VT::MB)[s];
-                    const int vids[4] = {ids4.x, ids4.y, ids4.z, ids4.w};
-#pragma unroll
-                    for (int r = 0; r < 4; ++r)
-                        oh[r] = clamp_id(vids[r], P.v.nc) == lane ? (_Float16)1.0f : (_Float16)0.0f;
+                    // bytes of x are zero where a token's id equals this lane; ids
+                    // and lanes are below 64, so 0x40 - byte keeps bit 6 exactly
+                    // there without borrows, and the perms widen those bytes to
+                    // fp16 2.0 (0x4000): the mass accumulates twice its value
+                    const uint32_t x = SV.ids4(s) ^ lane_bytes;
+                    const uint32_t e = (0x40404040u - x) & 0x40404040u;
+                    oh = __builtin_bit_cast(half4_t, make_uint2(__builtin_amdgcn_perm(0u, e, 0x010C000Cu),
+                                                                __builtin_amdgcn_perm(0u, e, 0x030C020Cu)));
                 }
 #pragma unroll
                 for (int hs = 0; hs < NH; ++hs) {
@@ -777,7 +789,7 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
     }
     float bt[G];
 #pragma unroll
-    for (int g = 0; g < G; ++g) bt[g] = VT::CENT ? accb[g >> 2][g & 3] : 0.0f;
+    for (int g = 0; g < G; ++g) bt[g] = VT::CENT ? 0.5f * accb[g >> 2][g & 3] : 0.0f;  // one-hot entries were 2
     __syncthreads();  // centroid table and stages no longer needed
     float* rec = reinterpret_cast<float*>(smem) + wave * G * kPartStride;
 #pragma unroll
