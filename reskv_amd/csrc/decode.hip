@@ -40,7 +40,8 @@ constexpr int kPartStride = kDim + kMaxClusters + 2;  // cross-wave merge record
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr int kVPitch = kDim + 8;  // halves per token row of the V transpose tile (conflict-free writes)
-constexpr int kCPitch = kDim + 8;  // halves per row of the LDS key-centroid table (staggered banks)
+constexpr int kCPitch = kDim + 4;  // halves per row of the LDS key-centroid table (66 dwords: 8-byte reads spread over the banks)
+constexpr int kRowPad = 8;         // bytes after each staged payload row (34-dword rows for 128-byte payloads)
 
 typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
@@ -105,6 +106,18 @@ __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_ex
 // ---------------------------------------------------------------------------
 // tile staging: global -> registers (prefetch) -> LDS
 // ---------------------------------------------------------------------------
+// 16-byte LDS accesses issued as two 8-byte halves
+__device__ __forceinline__ uint4 lds_ld16(const void* p) {
+    const uint2* q = reinterpret_cast<const uint2*>(p);
+    const uint2 a = q[0], b = q[1];
+    return make_uint4(a.x, a.y, b.x, b.y);
+}
+__device__ __forceinline__ void lds_st16(void* p, uint4 v) {
+    uint2* q = reinterpret_cast<uint2*>(p);
+    q[0] = make_uint2(v.x, v.y);
+    q[1] = make_uint2(v.z, v.w);
+}
+
 template <int F>
 struct Prefetch {
     uint4 pay[Traits<F>::PQ];
@@ -163,14 +176,15 @@ __device__ __forceinline__ void prefetch(const WaveSrc<F>& W, int pb, int off, i
         P.sc = h2f(__builtin_amdgcn_raw_buffer_load_b16(W.scale, tok >= 0 ? tok * 2 : kOut, 0, 0));
 }
 
-// Stage layout (bytes): payload [16][pb + 16] | meta [16][MB] | ids int32[16] |
+// Stage layout (bytes): payload [16][pb + kRowPad] | meta [16][MB] | ids int32[16] |
 // scale f32[16] | ids uint8[16].  Ids are stored clamped to [0, nc - 1]; the
-// byte copy feeds the one-hot operand of the cluster mass.  The 16-byte pad
+// byte copy feeds the one-hot operand of the cluster mass.  The 8-byte pad
 // staggers consecutive payload rows over the LDS banks (16 lanes read 16
-// different rows at similar offsets).
+// different rows at similar offsets); rows are 8-byte aligned, so wide stage
+// accesses are done as 8-byte halves.
 template <int F>
 __host__ __device__ constexpr int stage_bytes(int pb) {
-    return kTile * (pb + 16) + kTile * Traits<F>::MB + 2 * kTile * 4 + kTile;
+    return kTile * (pb + kRowPad) + kTile * Traits<F>::MB + 2 * kTile * 4 + kTile;
 }
 
 // LDS byte offsets of this lane's prefetch pieces inside the stage (piece
@@ -182,7 +196,7 @@ __device__ __forceinline__ void stage_slots(int pb, int lane, int* slot) {
 #pragma unroll
     for (int i = 0; i < Traits<F>::PQ; ++i) {
         const int q = lane + kWave * i;
-        slot[i] = q < kTile * per_tok ? (q / per_tok) * (pb + 16) + (q % per_tok) * 16 : -1;
+        slot[i] = q < kTile * per_tok ? (q / per_tok) * (pb + kRowPad) + (q % per_tok) * 16 : -1;
     }
 }
 
@@ -192,10 +206,10 @@ __device__ __forceinline__ void stage_store(const Prefetch<F>& P, uint8_t* st, i
     using Tr = Traits<F>;
 #pragma unroll
     for (int i = 0; i < Tr::PQ; ++i)
-        if (slot[i] >= 0) *reinterpret_cast<uint4*>(st + slot[i]) = P.pay[i];
-    uint8_t* meta = st + kTile * (pb + 16);
+        if (slot[i] >= 0) lds_st16(st + slot[i], P.pay[i]);
+    uint8_t* meta = st + kTile * (pb + kRowPad);
     if (lane < kTile) {
-        if constexpr (Tr::MB == 16) reinterpret_cast<uint4*>(meta)[lane] = P.meta;
+        if constexpr (Tr::MB == 16) lds_st16(meta + 16 * lane, P.meta);
         if constexpr (Tr::MB == 8) reinterpret_cast<uint2*>(meta)[lane] = make_uint2(P.meta.x, P.meta.y);
         int* ids = reinterpret_cast<int*>(meta + kTile * Tr::MB);
         const int cid = P.id < 0 ? 0 : (P.id >= nc ? nc - 1 : P.id);  // compression.cu:83-84
@@ -205,10 +219,11 @@ __device__ __forceinline__ void stage_store(const Prefetch<F>& P, uint8_t* st, i
     }
 }
 
+
 template <int F>
 struct StageView {
     const uint8_t* st;
-    int pp;  // payload row pitch (pb + 16)
+    int pp;  // payload row pitch (pb + kRowPad)
     __device__ const uint8_t* row(int t) const { return st + t * pp; }
     __device__ const uint8_t* meta(int t) const { return st + kTile * pp + t * Traits<F>::MB; }
     __device__ int id(int t) const {
@@ -260,13 +275,13 @@ __device__ __forceinline__ float half_hi(uint32_t w) { return h2f((uint16_t)(w >
 __device__ __forceinline__ int popc(uint32_t v) { return __builtin_popcount(v); }
 __device__ __forceinline__ int clamp_id(int id, int nc) { return id < 0 ? 0 : (id >= nc ? nc - 1 : id); }
 
-// Kept values of one 4-channel run as two fp16 pairs.  The window needs a
-// third dword only for a full run (pattern 15) starting at an odd rank.
+// Kept values of one 4-channel run as two fp16 pairs.  The window's third
+// dword matters only for a full run (pattern 15) starting at an odd rank; it
+// is read unconditionally (the 16-byte row pad keeps it inside the stage), so
+// the runs stay branch-free and their LDS reads can be issued together.
 __device__ __forceinline__ void run_h(const uint8_t* row, int base, const uint32_t* tab, uint32_t v, uint32_t* out) {
     const uint32_t* dw = reinterpret_cast<const uint32_t*>(row) + (base >> 1);
-    const uint32_t d0 = dw[0], d1 = dw[1];
-    uint32_t d2 = 0;
-    if ((base & 1) && v == 15u) d2 = dw[2];
+    const uint32_t d0 = dw[0], d1 = dw[1], d2 = dw[2];
     const uint32_t sh = (uint32_t)(base & 1) * 16u;
     const uint32_t w0 = __builtin_amdgcn_alignbit(d1, d0, sh);
     const uint32_t w1 = __builtin_amdgcn_alignbit(d2, d1, sh);
@@ -296,7 +311,7 @@ __device__ __forceinline__ void residual_h(const StageView<F>& S, int t, int g, 
         // words: channels 0..63 in (m.y:m.x), 64..127 in (m.w:m.z), MSB-first
         // (reference.py:22-26); group g's 16 channels are the (g odd ? low : high)
         // half of dword (g < 2 ? high : low), channel 16g + c at field bit 15 - c
-        const uint4 m = *reinterpret_cast<const uint4*>(S.meta(t));
+        const uint4 m = lds_ld16(S.meta(t));
         const uint32_t sh = (g & 1) ? 0u : 16u;
         const uint32_t f0 = ((g < 2 ? m.y : m.x) >> sh) & 0xFFFFu;
         const uint32_t f1 = ((g < 2 ? m.w : m.z) >> sh) & 0xFFFFu;
@@ -313,7 +328,7 @@ __device__ __forceinline__ void residual_h(const StageView<F>& S, int t, int g, 
     } else if constexpr (F == D_TILED || F == D_TILED_W || F == D_STRUCT16) {
         // word w = code(tile 2w) | code(tile 2w+1) << 16 (reference.py:36-47);
         // group g covers tiles g and 4 + g
-        const uint4 m = *reinterpret_cast<const uint4*>(S.meta(t));
+        const uint4 m = lds_ld16(S.meta(t));
         const uint32_t sh = (uint32_t)(g & 1) * 16u;
         uint32_t f0 = ((g < 2 ? m.x : m.y) >> sh) & 0xFFFFu;
         uint32_t f1 = ((g < 2 ? m.z : m.w) >> sh) & 0xFFFFu;
@@ -358,7 +373,8 @@ __device__ __forceinline__ void residual_h(const StageView<F>& S, int t, int g, 
         }
     } else if constexpr (F == D_DENSE) {
         const uint4* r = reinterpret_cast<const uint4*>(row);
-        const uint4 a = r[2 * g], b = r[2 * g + 1], c = r[8 + 2 * g], d = r[9 + 2 * g];
+        const uint4 a = lds_ld16(r + 2 * g), b = lds_ld16(r + 2 * g + 1), c = lds_ld16(r + 8 + 2 * g),
+                    d = lds_ld16(r + 9 + 2 * g);
         const uint32_t v[16] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w, c.x, c.y, c.z, c.w, d.x, d.y, d.z, d.w};
 #pragma unroll
         for (int i = 0; i < 16; ++i) h[i] = v[i];
@@ -386,7 +402,7 @@ __device__ __forceinline__ void residual_f(const StageView<F>& S, int t, int g, 
         // 1 of 4 per subgroup of four channels: 2-bit position, signed nibble
         // code, fp16 scale (reference.py:27-35); group g holds subgroups
         // 4g..4g+3 and 16+4g..16+4g+3
-        const uint4 qp = *reinterpret_cast<const uint4*>(row);
+        const uint4 qp = lds_ld16(row);
         const uint2 qm = *reinterpret_cast<const uint2*>(S.meta(t));
         const uint32_t qw[4] = {qp.x, qp.y, qp.z, qp.w};
 #pragma unroll
@@ -413,7 +429,7 @@ __device__ __forceinline__ void key_values(const StageView<F>& S, int t, int g, 
     if constexpr (Traits<F>::CENT) {
         const int kid = S.id(t);  // clamped when staged
         const uint4* cr = reinterpret_cast<const uint4*>(s_cent + kid * kCPitch);
-        const uint4 a = cr[2 * g], b = cr[2 * g + 1], d = cr[8 + 2 * g], e = cr[9 + 2 * g];
+        const uint4 a = lds_ld16(cr + 2 * g), b = lds_ld16(cr + 2 * g + 1), d = lds_ld16(cr + 8 + 2 * g), e = lds_ld16(cr + 9 + 2 * g);
         const uint32_t v[16] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w, d.x, d.y, d.z, d.w, e.x, e.y, e.z, e.w};
 #pragma unroll
         for (int i = 0; i < 16; ++i) c[i] = v[i];
@@ -527,8 +543,8 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
     uint16_t* my_vt = my_p + kTile * G;
     uint8_t* st_k = smem + P.stage_off + wave * (P.stage_k + P.stage_v);
     uint8_t* st_v = st_k + P.stage_k;
-    const StageView<KF> SK{st_k, P.k.pb + 16};
-    const StageView<VF> SV{st_v, P.v.pb + 16};
+    const StageView<KF> SK{st_k, P.k.pb + kRowPad};
+    const StageView<VF> SV{st_v, P.v.pb + kRowPad};
     const GroupMask gm = group_mask(grp);
     if (threadIdx.x < kLutWords) {
         const uint32_t i = threadIdx.x;
@@ -538,7 +554,7 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
     if constexpr (KT::CENT) {
         const uint4* kc = reinterpret_cast<const uint4*>(P.k.cent + bh * P.k.cs * kDim);
         for (int i = threadIdx.x; i < P.k.nc * (kDim / 8); i += kThreads)
-            *reinterpret_cast<uint4*>(s_cent + (i >> 4) * kCPitch + 8 * (i & 15)) = kc[i];
+            lds_st16(s_cent + (i >> 4) * kCPitch + 8 * (i & 15), kc[i]);
     }
 
     // rotated, pre-scaled query values of this lane's channels for heads 4 hs + hj
@@ -686,10 +702,10 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
             uint32_t hv[16];
             value_halves<VF>(SV, t, grp, P.v.width, gm, s_lut, hv);
             uint4* vr = reinterpret_cast<uint4*>(my_vt + t * kVPitch + 16 * grp);
-            vr[0] = make_uint4(hv[0], hv[1], hv[2], hv[3]);
-            vr[1] = make_uint4(hv[4], hv[5], hv[6], hv[7]);
-            vr[8] = make_uint4(hv[8], hv[9], hv[10], hv[11]);
-            vr[9] = make_uint4(hv[12], hv[13], hv[14], hv[15]);
+            lds_st16(vr + 0, make_uint4(hv[0], hv[1], hv[2], hv[3]));
+            lds_st16(vr + 1, make_uint4(hv[4], hv[5], hv[6], hv[7]));
+            lds_st16(vr + 8, make_uint4(hv[8], hv[9], hv[10], hv[11]));
+            lds_st16(vr + 9, make_uint4(hv[12], hv[13], hv[14], hv[15]));
         }
 
         // ---- online softmax over the tile: one exponential per lane ----
