@@ -252,7 +252,8 @@ struct StageView {
 // bitmaps, one for LSB-first tile masks).  The ranks of a lane's runs follow
 // from the first one by popcounts of the patterns.
 // ---------------------------------------------------------------------------
-constexpr int kLutWords = 64;  // [msb|lsb][pattern][lo|hi]
+constexpr int kLutWords = 64;        // [msb|lsb][pattern][lo|hi]
+constexpr int kStructLutWords = 160;  // 4:16 tiles: [start rank 0..4][pattern][lo|hi]
 
 // v_perm selector bytes placing window halves on channels 0..3 of a run
 // (byte 12 selects zero).  msb: pattern bit 3-j = channel j (bitmaps);
@@ -270,6 +271,21 @@ __host__ __device__ constexpr uint32_t perm_selector(uint32_t v, bool msb, int h
     return sel;
 }
 
+// Selectors for a 4:16 tile: the tile's four values are one 8-byte word, and a
+// run whose first kept value has rank `rank` takes bytes 2 (rank + i) of that
+// word directly (LSB-first pattern, bit j = channel j).
+__host__ __device__ constexpr uint32_t struct_selector(uint32_t v, uint32_t rank, int half) {
+    uint32_t sel = 0;
+    for (int jj = 0; jj < 2; ++jj) {
+        const int j = 2 * half + jj;
+        const uint32_t pos = rank + (uint32_t)__builtin_popcount(v & ((1u << j) - 1u));
+        const bool kept = ((v >> j) & 1u) && pos < 4;
+        const uint32_t b0 = kept ? 2 * pos : 12u, b1 = kept ? 2 * pos + 1 : 12u;
+        sel |= (b0 | (b1 << 8)) << (16 * jj);
+    }
+    return sel;
+}
+
 __device__ __forceinline__ float half_lo(uint32_t w) { return h2f((uint16_t)(w & 0xFFFFu)); }
 __device__ __forceinline__ float half_hi(uint32_t w) { return h2f((uint16_t)(w >> 16)); }
 __device__ __forceinline__ int popc(uint32_t v) { return __builtin_popcount(v); }
@@ -277,8 +293,9 @@ __device__ __forceinline__ int clamp_id(int id, int nc) { return id < 0 ? 0 : (i
 
 // Kept values of one 4-channel run as two fp16 pairs.  The window's third
 // dword matters only for a full run (pattern 15) starting at an odd rank; it
-// is read unconditionally (the 16-byte row pad keeps it inside the stage), so
-// the runs stay branch-free and their LDS reads can be issued together.
+// is read unconditionally (a read past a row's pad stays inside the stage: the
+// next row, or the metadata after the last row), so the runs stay branch-free
+// and their LDS reads can be issued together.
 __device__ __forceinline__ void run_h(const uint8_t* row, int base, const uint32_t* tab, uint32_t v, uint32_t* out) {
     const uint32_t* dw = reinterpret_cast<const uint32_t*>(row) + (base >> 1);
     const uint32_t d0 = dw[0], d1 = dw[1], d2 = dw[2];
@@ -334,7 +351,8 @@ __device__ __forceinline__ void residual_h(const StageView<F>& S, int t, int g, 
         uint32_t f1 = ((g < 2 ? m.z : m.w) >> sh) & 0xFFFFu;
         if constexpr (F == D_STRUCT16) {
             // four ascending in-tile channel indices -> 16-bit mask; the tile's
-            // four values are one 8-byte word, windows come from 64-bit shifts
+            // four values are one 8-byte word, and the (rank, pattern) selectors
+            // pick each run's values from it
             uint32_t k0 = 0, k1 = 0;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
@@ -343,19 +361,18 @@ __device__ __forceinline__ void residual_h(const StageView<F>& S, int t, int g, 
             }
             const uint2 pa = reinterpret_cast<const uint2*>(row)[g];
             const uint2 pb = reinterpret_cast<const uint2*>(row)[4 + g];
-            const uint64_t wa = (uint64_t)pa.x | ((uint64_t)pa.y << 32);
-            const uint64_t wb = (uint64_t)pb.x | ((uint64_t)pb.y << 32);
+            const uint32_t* slut = lut + kLutWords;
             int r0 = 0, r1 = 0;
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
                 const uint32_t a = (k0 >> (4 * u)) & 15u, c = (k1 >> (4 * u)) & 15u;
-                const uint64_t xa = wa >> ((16 * r0) & 63), xb = wb >> ((16 * r1) & 63);
-                const uint2 sa = *reinterpret_cast<const uint2*>(lut + 32 + 2 * a);
-                const uint2 sb = *reinterpret_cast<const uint2*>(lut + 32 + 2 * c);
-                h[2 * u] = __builtin_amdgcn_perm((uint32_t)(xa >> 32), (uint32_t)xa, sa.x);
-                h[2 * u + 1] = __builtin_amdgcn_perm((uint32_t)(xa >> 32), (uint32_t)xa, sa.y);
-                h[8 + 2 * u] = __builtin_amdgcn_perm((uint32_t)(xb >> 32), (uint32_t)xb, sb.x);
-                h[8 + 2 * u + 1] = __builtin_amdgcn_perm((uint32_t)(xb >> 32), (uint32_t)xb, sb.y);
+                // ranks stay within 0..4: the mask has at most four bits
+                const uint2 sa = *reinterpret_cast<const uint2*>(slut + 2 * (16 * r0 + (int)a));
+                const uint2 sb = *reinterpret_cast<const uint2*>(slut + 2 * (16 * r1 + (int)c));
+                h[2 * u] = __builtin_amdgcn_perm(pa.y, pa.x, sa.x);
+                h[2 * u + 1] = __builtin_amdgcn_perm(pa.y, pa.x, sa.y);
+                h[8 + 2 * u] = __builtin_amdgcn_perm(pb.y, pb.x, sb.x);
+                h[8 + 2 * u + 1] = __builtin_amdgcn_perm(pb.y, pb.x, sb.y);
                 r0 += popc(a);
                 r1 += popc(c);
             }
@@ -549,6 +566,9 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
     if (threadIdx.x < kLutWords) {
         const uint32_t i = threadIdx.x;
         s_lut[i] = perm_selector((i >> 1) & 15u, i < 32, (int)(i & 1));
+    } else if (threadIdx.x < kLutWords + kStructLutWords) {
+        const uint32_t i = threadIdx.x - kLutWords;
+        s_lut[kLutWords + i] = struct_selector((i >> 1) & 15u, i >> 5, (int)(i & 1));
     }
 
     if constexpr (KT::CENT) {
@@ -1217,7 +1237,7 @@ int run_decode(const void* q, int kf, const DTensor& k, int vf, const DTensor& v
     const int cent_bytes = cent ? k.nc * kCPitch * 2 : 0;
     const int region0 = cent_bytes > merge_bytes ? cent_bytes : merge_bytes;
     p.lut_off = region0;
-    p.p_off = p.lut_off + kLutWords * 4;
+    p.p_off = p.lut_off + (kLutWords + kStructLutWords) * 4;
     p.stage_off = p.p_off + kWaves * (kTile * G + kTile * kVPitch) * 2;
     const size_t shm = (size_t)p.stage_off + (size_t)kWaves * (p.stage_k + p.stage_v);
     RESKV_REQUIRE(shm <= 160 * 1024, "decode LDS requirement %zu exceeds 160 KiB", shm);

@@ -111,6 +111,26 @@ class ResKVForCausalLM(LlamaForCausalLM):
     def _supports_default_dynamic_cache(cls):
         return False
 
+    @classmethod
+    def from_pretrained(cls, pretrained_model_name_or_path, *args, kernel_config=None, **kwargs):
+        """``from_pretrained(path, kernel_config=ResKVKernelConfig(...))`` as in the reference.
+
+        transformers 5 reserves the ``kernel_config`` keyword for its hub
+        kernels; a ResKV configuration is handed over through the model config
+        (``reskv_kernel_config``, which ``__init__`` reads), any other value
+        goes on to transformers."""
+        if isinstance(kernel_config, ResKVKernelConfig):
+            from transformers import AutoConfig
+
+            config = kwargs.pop("config", None)
+            if config is None:
+                config = AutoConfig.from_pretrained(pretrained_model_name_or_path)
+            config.reskv_kernel_config = kernel_config.to_dict()
+            kwargs["config"] = config
+        elif kernel_config is not None:
+            kwargs["kernel_config"] = kernel_config
+        return super().from_pretrained(pretrained_model_name_or_path, *args, **kwargs)
+
     def _frequencies(self):
         """The model's RoPE inverse frequencies in fp32 (recomputed when ``.half()`` cast the buffer)."""
         rotary = self.model.rotary_emb

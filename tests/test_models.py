@@ -81,3 +81,16 @@ def test_forward_checks():
         cache = model(ids).past_key_values
         with pytest.raises(ValueError, match="single-token"):
             model(ids[:, :2], past_key_values=cache)
+
+
+def test_from_pretrained_takes_the_kernel_config(tmp_path):
+    """transformers 5 reserves ``kernel_config`` in from_pretrained; the ResKV settings still arrive."""
+    LlamaForCausalLM(_config()).save_pretrained(tmp_path)
+    cfg = ResKVKernelConfig(sparsity=0.5, num_clusters=16)
+    model = ResKVForCausalLM.from_pretrained(tmp_path, kernel_config=cfg)
+    assert model.kernel_config == cfg
+    again = ResKVForCausalLM.from_pretrained(tmp_path)  # defaults when the checkpoint stores none
+    assert again.kernel_config == ResKVKernelConfig()
+    model.save_pretrained(tmp_path / "saved")
+    reloaded = ResKVForCausalLM.from_pretrained(tmp_path / "saved")  # settings stored with the checkpoint
+    assert reloaded.kernel_config == cfg
