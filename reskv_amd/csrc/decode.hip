@@ -563,6 +563,28 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
     const StageView<KF> SK{st_k, P.k.pb + kRowPad};
     const StageView<VF> SV{st_v, P.v.pb + kRowPad};
     const GroupMask gm = group_mask(grp);
+
+    // The first tiles' loads go out before the set-up work below, which then
+    // overlaps their latency.
+    const int ntiles = (t1 - t0 + kTile - 1) / kTile;
+    const WaveSrc<KF> wk = wave_src<KF>(P.k, bh * P.k.ts + t0, t1 - t0);
+    const WaveSrc<VF> wv = wave_src<VF>(P.v, bh * P.v.ts + t0, t1 - t0);
+    // Tiles are prefetched kDepth ahead into register buffers used in turn
+    // (two for formats of at most one 16-byte piece per lane and tensor, whose
+    // short tiles would otherwise wait on the load latency; one otherwise).
+    constexpr int kDepth = (KT::PQ + VT::PQ <= 2 && G <= 4) ? 2 : 1;
+    Prefetch<KF> pk[kDepth];
+    Prefetch<VF> pv[kDepth];
+#pragma unroll
+    for (int d = 0; d < kDepth; ++d) {
+        pk[d] = Prefetch<KF>{};
+        pv[d] = Prefetch<VF>{};
+        if (d < ntiles) {
+            prefetch<KF>(wk, P.k.pb, d * kTile, lane, pk[d]);
+            prefetch<VF>(wv, P.v.pb, d * kTile, lane, pv[d]);
+        }
+    }
+
     if (threadIdx.x < kLutWords) {
         const uint32_t i = threadIdx.x;
         s_lut[i] = perm_selector((i >> 1) & 15u, i < 32, (int)(i & 1));
@@ -638,24 +660,6 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
     stage_slots<VF>(P.v.pb, lane, vslot);
     __syncthreads();
 
-    const int ntiles = (t1 - t0 + kTile - 1) / kTile;
-    const WaveSrc<KF> wk = wave_src<KF>(P.k, bh * P.k.ts + t0, t1 - t0);
-    const WaveSrc<VF> wv = wave_src<VF>(P.v, bh * P.v.ts + t0, t1 - t0);
-    // Tiles are prefetched kDepth ahead into register buffers used in turn
-    // (two for formats of at most one 16-byte piece per lane and tensor, whose
-    // short tiles would otherwise wait on the load latency; one otherwise).
-    constexpr int kDepth = (KT::PQ + VT::PQ <= 2 && G <= 4) ? 2 : 1;
-    Prefetch<KF> pk[kDepth];
-    Prefetch<VF> pv[kDepth];
-#pragma unroll
-    for (int d = 0; d < kDepth; ++d) {
-        pk[d] = Prefetch<KF>{};
-        pv[d] = Prefetch<VF>{};
-        if (d < ntiles) {
-            prefetch<KF>(wk, P.k.pb, d * kTile, lane, pk[d]);
-            prefetch<VF>(wv, P.v.pb, d * kTile, lane, pv[d]);
-        }
-    }
     auto tile_body = [&](int tile, Prefetch<KF>& fk, Prefetch<VF>& fv) {
         const int tb = t0 + tile * kTile;
         const int n = min(kTile, t1 - tb);
@@ -869,11 +873,15 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
 }
 
 // One workgroup (256 threads) per (batch, query head) combines the split
-// partials (log2 domain).  The residual sums are read as float4 by 8 groups of
-// 32 threads (split s goes to group s % 8), the cluster masses by 16 groups of
-// 16 threads, so a thread keeps at most S/8 independent loads in flight;
-// the groups are then reduced through LDS.
+// partials (log2 domain).  Every global load is issued before the split
+// weights are known, so the kernel waits on memory once: the residual sums are
+// read as float4 by 8 groups of 32 threads (split s goes to group s % 8), the
+// cluster masses by 16 groups of 16 threads, the first eight (resp. four)
+// splits of a thread into registers, and the Value centroids into LDS.  The
+// groups are then reduced through LDS and the centroids folded in.
 constexpr int kMergeThreads = 256;
+constexpr int kMergeRegD = 8;  // residual-sum splits per thread held in registers
+constexpr int kMergeRegB = 4;  // cluster-mass splits per thread held in registers
 
 __global__ void __launch_bounds__(kMergeThreads) decode_merge_kernel(
     const float* __restrict__ pm, const float* __restrict__ pl, const float* __restrict__ pdelta,
@@ -883,17 +891,48 @@ __global__ void __launch_bounds__(kMergeThreads) decode_merge_kernel(
     __shared__ float s_red[kMergeThreads / kWave];
     __shared__ float4 s_d[8][kDim / 4];
     __shared__ float4 s_b[16][kMaxClusters / 4];
+    __shared__ float s_beta[kMaxClusters];
+    __shared__ uint4 s_vc[kMaxClusters * kDim / 8];  // fp16 Value centroids [c][128]
     const long bq = blockIdx.x;  // b * Hq + hq
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int G = Hq / H;
     const long bh = (bq / Hq) * H + (bq % Hq) / G;
     const float* m_row = pm + bq * splits;
     const float* l_row = pl + bq * splits;
+    const int dg = tid >> 5, dq = tid & 31;  // residual sums: split group, channel quad
+    const int bg = tid >> 4, bq4 = tid & 15;  // cluster masses: split group, cluster quad
+    const float4* dbase = reinterpret_cast<const float4*>(pdelta + (bq * splits) * kDim) + dq;
+    const float4* bbase = reinterpret_cast<const float4*>(pbeta + (bq * splits) * kMaxClusters) + bq4;
+    const float4 zero4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+
+    // 0) loads that do not depend on the split weights
+    const bool one_pass = splits <= kMergeThreads;  // one split per thread for the maximum and weights
+    float m0 = -INFINITY, l0 = 0.0f;
+    if (one_pass && tid < splits) {
+        m0 = m_row[tid];
+        l0 = l_row[tid];
+    }
+    float4 dv[kMergeRegD], bv[kMergeRegB];
+#pragma unroll
+    for (int i = 0; i < kMergeRegD; ++i) {
+        const int sp = dg + 8 * i;
+        dv[i] = sp < splits ? dbase[(long)sp * (kDim / 4)] : zero4;
+    }
+#pragma unroll
+    for (int i = 0; i < kMergeRegB; ++i) {
+        const int sp = bg + 16 * i;
+        bv[i] = sp < splits ? bbase[(long)sp * (kMaxClusters / 4)] : zero4;
+    }
+    if (vcent != nullptr) {
+        const uint4* vc = reinterpret_cast<const uint4*>(vcent + bh * vcs * kDim);
+        for (int i = tid; i < vnc * (kDim / 8); i += kMergeThreads) s_vc[i] = vc[i];
+    }
 
     // 1) common maximum over the non-empty splits
-    float mx = -INFINITY;
-    for (int s = tid; s < splits; s += kMergeThreads)
-        if (l_row[s] > 0.0f) mx = fmaxf(mx, m_row[s]);
+    float mx = one_pass ? (l0 > 0.0f ? m0 : -INFINITY) : -INFINITY;
+    if (!one_pass)
+        for (int sp = tid; sp < splits; sp += kMergeThreads)
+            if (l_row[sp] > 0.0f) mx = fmaxf(mx, m_row[sp]);
     mx = wave_max(mx);
     if (lane == 0) s_red[wave] = mx;
     __syncthreads();
@@ -902,48 +941,75 @@ __global__ void __launch_bounds__(kMergeThreads) decode_merge_kernel(
 
     // 2) split weights and the normaliser
     float lsum = 0.0f;
-    for (int s = tid; s < splits; s += kMergeThreads) {
-        const float lw = l_row[s];
-        const float w = lw > 0.0f ? exp2_fast(m_row[s] - mx) : 0.0f;
-        s_w[s] = w;
-        lsum += lw * w;
+    if (one_pass) {
+        if (tid < splits) {
+            const float w = l0 > 0.0f ? exp2_fast(m0 - mx) : 0.0f;
+            s_w[tid] = w;
+            lsum = l0 * w;
+        }
+    } else {
+        for (int sp = tid; sp < splits; sp += kMergeThreads) {
+            const float lw = l_row[sp];
+            const float w = lw > 0.0f ? exp2_fast(m_row[sp] - mx) : 0.0f;
+            s_w[sp] = w;
+            lsum += lw * w;
+        }
     }
     lsum = wave_sum(lsum);
     if (lane == 0) s_red[wave] = lsum;
     __syncthreads();
     lsum = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
 
-    // 3) residual sums: thread = (split group tid / 32, channel quad tid % 32)
+    // 3) weighted residual sums and cluster masses per split group
     {
-        const int grp = tid >> 5, cq = tid & 31;
-        const float4* base = reinterpret_cast<const float4*>(pdelta + (bq * splits) * kDim) + cq;
-        float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-#pragma unroll 8
-        for (int s = grp; s < splits; s += 8) {
-            const float w = s_w[s];
-            const float4 d = base[(long)s * (kDim / 4)];
+        float4 acc = zero4;
+#pragma unroll
+        for (int i = 0; i < kMergeRegD; ++i) {
+            const int sp = dg + 8 * i;
+            const float w = sp < splits ? s_w[sp] : 0.0f;
+            acc.x = fmaf(w, dv[i].x, acc.x);
+            acc.y = fmaf(w, dv[i].y, acc.y);
+            acc.z = fmaf(w, dv[i].z, acc.z);
+            acc.w = fmaf(w, dv[i].w, acc.w);
+        }
+        for (int sp = dg + 8 * kMergeRegD; sp < splits; sp += 8) {
+            const float w = s_w[sp];
+            const float4 d = dbase[(long)sp * (kDim / 4)];
             acc.x = fmaf(w, d.x, acc.x);
             acc.y = fmaf(w, d.y, acc.y);
             acc.z = fmaf(w, d.z, acc.z);
             acc.w = fmaf(w, d.w, acc.w);
         }
-        s_d[grp][cq] = acc;
+        s_d[dg][dq] = acc;
+        float4 accb = zero4;
+#pragma unroll
+        for (int i = 0; i < kMergeRegB; ++i) {
+            const int sp = bg + 16 * i;
+            const float w = sp < splits ? s_w[sp] : 0.0f;
+            accb.x = fmaf(w, bv[i].x, accb.x);
+            accb.y = fmaf(w, bv[i].y, accb.y);
+            accb.z = fmaf(w, bv[i].z, accb.z);
+            accb.w = fmaf(w, bv[i].w, accb.w);
+        }
+        for (int sp = bg + 16 * kMergeRegB; sp < splits; sp += 16) {
+            const float w = s_w[sp];
+            const float4 d = bbase[(long)sp * (kMaxClusters / 4)];
+            accb.x = fmaf(w, d.x, accb.x);
+            accb.y = fmaf(w, d.y, accb.y);
+            accb.z = fmaf(w, d.z, accb.z);
+            accb.w = fmaf(w, d.w, accb.w);
+        }
+        s_b[bg][bq4] = accb;
     }
-    // 4) cluster mass: thread = (split group tid / 16, cluster quad tid % 16)
-    {
-        const int grp = tid >> 4, cq = tid & 15;
-        const float4* base = reinterpret_cast<const float4*>(pbeta + (bq * splits) * kMaxClusters) + cq;
-        float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-#pragma unroll 4
-        for (int s = grp; s < splits; s += 16) {
-            const float w = s_w[s];
-            const float4 d = base[(long)s * (kMaxClusters / 4)];
-            acc.x = fmaf(w, d.x, acc.x);
-            acc.y = fmaf(w, d.y, acc.y);
-            acc.z = fmaf(w, d.z, acc.z);
-            acc.w = fmaf(w, d.w, acc.w);
-        }
-        s_b[grp][cq] = acc;
+    __syncthreads();
+    // 4) cluster masses summed over the 16 groups (threads 128..191)
+    if (tid >= kDim && tid < kDim + kMaxClusters) {
+        const int c = tid - kDim;
+        const float* sb = reinterpret_cast<const float*>(s_b);
+        float beta = 0.0f;
+#pragma unroll
+        for (int g2 = 0; g2 < 16; ++g2) beta += sb[g2 * kMaxClusters + c];
+        s_beta[c] = beta;
     }
     __syncthreads();
     // 5) fold sum_c beta_c c_v[c], normalise (threads 0..127: one channel each)
@@ -953,14 +1019,8 @@ __global__ void __launch_bounds__(kMergeThreads) decode_merge_kernel(
 #pragma unroll
         for (int g2 = 0; g2 < 8; ++g2) acc += sd[g2 * kDim + tid];
         if (vcent != nullptr) {
-            const float* sb = reinterpret_cast<const float*>(s_b);
-            const uint16_t* vc = vcent + bh * vcs * kDim + tid;
-            for (int c = 0; c < vnc; ++c) {
-                float beta = 0.0f;
-#pragma unroll
-                for (int g2 = 0; g2 < 16; ++g2) beta += sb[g2 * kMaxClusters + c];
-                acc = fmaf(beta, h2f(vc[c * kDim]), acc);
-            }
+            const uint16_t* vc = reinterpret_cast<const uint16_t*>(s_vc) + tid;
+            for (int c = 0; c < vnc; ++c) acc = fmaf(s_beta[c], h2f(vc[c * kDim]), acc);
         }
         const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
         out[bq * kDim + tid] = f2h(acc * inv);
