@@ -188,6 +188,18 @@ int reskv_merge_recent_qk(const void* comp_out, const float* comp_m, const float
                           int B, int Hq, int H, int Tr, int r_stride, float scaling, void* out,
                           void* stream);
 
+/* reskv_decode_rope followed by reskv_merge_recent_qk in two kernel launches
+ * instead of three: the split merge joins the recent tokens before it writes
+ * out (fp16 [B*Hq,128]; the joint m, l are not returned).  The result is
+ * bitwise that of the two calls.  The reference runs the same two steps as
+ * separate ops (reskv/_attention.py:117-143 after cluster_mass.cu:1177-1296);
+ * this entry point serves decode loops, where every launch counts. */
+int reskv_decode_recent(const void* q, const reskv_ctensor* k, const reskv_ctensor* v,
+                        const float* inv_freq, const float* rope_table, int B, int Hq, int H, int T,
+                        int start_pos, int pos_q, float scaling, int splits, const void* q_rope,
+                        const void* k_recent, const void* v_recent, int Tr, int r_stride, void* out,
+                        void* workspace, int64_t workspace_bytes, void* stream);
+
 /* Dense fp16 decode attention (the uncompressed baseline at the same shapes):
  * q fp16 [B*Hq,128] pre-RoPE, k fp16 [B,H,*,128] pre-RoPE, v fp16 [B,H,*,128]:
  * the first T tokens of rows of t_stride tokens (t_stride<=0: T), so that a

@@ -337,10 +337,10 @@ class StepDecoder:
     a dense ring of recent tokens, without per-call validation or allocation.
 
     Descriptors, the RoPE table, the split workspace and the outputs are made
-    once for a CompressedKV; each ``run`` issues the fused decode
-    (``reskv_decode_rope``) and the in-place ring merge
-    (``reskv_merge_recent_qk`` over rows of ``ring_stride`` tokens).  The result
-    equals ``attention(query, cache, position=..., recent=(...))``."""
+    once for a CompressedKV; each ``run`` issues the fused decode and the
+    in-place ring merge (rows of ``ring_stride`` tokens) as two kernels
+    (``reskv_decode_recent``).  The result equals ``attention(query, cache,
+    position=..., recent=(...))``."""
 
     def __init__(self, cache, num_q_heads, scaling, inv_freq=None, rope_theta=500000.0, splits=0):
         self.cache = cache
@@ -361,24 +361,33 @@ class StepDecoder:
         self.l = torch.empty((rows,), dtype=torch.float32, device=dev)
         self.merged = torch.empty((rows, 128), dtype=torch.float16, device=dev)
 
-    def run(self, query, position, query_rot=None, ring_k=None, ring_v=None, ring_len=0, ring_stride=0):
+    def run(self, query, position, query_rot=None, ring_k=None, ring_v=None, ring_len=0, ring_stride=0, out=None):
         """query fp16 [B, Hq, 1, 128] pre-RoPE (contiguous); ring_k/ring_v fp16
         [B, Hk, ring_stride, 128] buffers whose first ring_len tokens are the
         recent window (rotated K, V); query_rot its rotated query.  Returns
-        fp16 [B, Hq, 1, 128] (a buffer reused by the next call)."""
+        fp16 [B, Hq, 1, 128]: ``out`` (contiguous fp16 with B * Hq * 128
+        elements) when given, else a buffer reused by the next call.  With a
+        recent window the split merge joins it in the same launch
+        (``reskv_decode_recent``)."""
         L = _lib.lib()
         stream = _stream(self.dev)
-        _lib.check(L.reskv_decode_rope(query.data_ptr(), self.kdesc, self.vdesc, self.freq.data_ptr(),
-                                       self.table.data_ptr(), self.b, self.nh, self.kh, self.t, 0, int(position),
-                                       self.scaling, self.splits, self.out.data_ptr(), self.m.data_ptr(),
-                                       self.l.data_ptr(), self.ws.data_ptr(), self.ws.numel(), stream), "decode")
+        if out is not None:
+            _require(out.dtype == torch.float16 and out.is_contiguous() and out.numel() == self.b * self.nh * 128
+                     and out.device == self.dev, "out must be contiguous fp16 with B * Hq * 128 elements")
         if ring_len <= 0:
-            return self.out.view(self.b, self.nh, 1, 128)
-        _lib.check(L.reskv_merge_recent_qk(self.out.data_ptr(), self.m.data_ptr(), self.l.data_ptr(),
-                                           query_rot.data_ptr(), ring_k.data_ptr(), ring_v.data_ptr(), self.b,
-                                           self.nh, self.kh, int(ring_len), int(ring_stride), self.scaling,
-                                           self.merged.data_ptr(), stream), "merge_recent")
-        return self.merged.view(self.b, self.nh, 1, 128)
+            dst = self.out if out is None else out
+            _lib.check(L.reskv_decode_rope(query.data_ptr(), self.kdesc, self.vdesc, self.freq.data_ptr(),
+                                           self.table.data_ptr(), self.b, self.nh, self.kh, self.t, 0, int(position),
+                                           self.scaling, self.splits, dst.data_ptr(), self.m.data_ptr(),
+                                           self.l.data_ptr(), self.ws.data_ptr(), self.ws.numel(), stream), "decode")
+            return dst.view(self.b, self.nh, 1, 128)
+        dst = self.merged if out is None else out
+        _lib.check(L.reskv_decode_recent(query.data_ptr(), self.kdesc, self.vdesc, self.freq.data_ptr(),
+                                         self.table.data_ptr(), self.b, self.nh, self.kh, self.t, 0, int(position),
+                                         self.scaling, self.splits, query_rot.data_ptr(), ring_k.data_ptr(),
+                                         ring_v.data_ptr(), int(ring_len), int(ring_stride), dst.data_ptr(),
+                                         self.ws.data_ptr(), self.ws.numel(), stream), "decode")
+        return dst.view(self.b, self.nh, 1, 128)
 
 
 def _make_cluster_mass():
@@ -518,12 +527,13 @@ def load_extension(family: str, plan: KernelPlan | None = None, device_index: in
     return _make_cluster_mass()
 
 
-def dense_decode(q, k, v, inv_freq, *, position, start_position=0, scaling=None, splits=0):
+def dense_decode(q, k, v, inv_freq, *, position, start_position=0, scaling=None, splits=0, out=None):
     """Dense fp16 decode attention baseline on the same split-K engine.
 
     q fp16 [B, Hq, 1, 128] pre-RoPE; k, v fp16 [B, H, T, 128] (k pre-RoPE),
     contiguous or the first T tokens of a preallocated [B, H, Tmax, 128] cache.
-    Returns fp16 [B, Hq, 1, 128].
+    Returns fp16 [B, Hq, 1, 128], written to ``out`` (contiguous fp16 with
+    B * Hq * 128 elements) when given.
     """
     _require(q.dtype == torch.float16 and k.dtype == torch.float16 and v.dtype == torch.float16, "fp16 inputs")
     dev = _dev_check(q, contiguous=True)
@@ -541,7 +551,11 @@ def dense_decode(q, k, v, inv_freq, *, position, start_position=0, scaling=None,
     # spare, while table reads would compete with it for the caches
     freq = _frequencies(inv_freq, 500000.0, dev)
     L = _lib.lib()
-    out = _empty((b * hq, 128), torch.float16, dev)
+    if out is None:
+        out = _empty((b * hq, 128), torch.float16, dev)
+    else:
+        _require(out.dtype == torch.float16 and out.is_contiguous() and out.numel() == b * hq * 128
+                 and out.device == dev, "out must be contiguous fp16 with B * Hq * 128 elements")
     ws = _workspace(L.reskv_decode_workspace_bytes(b, hq, h, t, int(splits)), dev)
     with torch.cuda.device(dev):
         _lib.check(L.reskv_decode_dense(q.data_ptr(), k.data_ptr(), v.data_ptr(), freq.data_ptr(), None,

@@ -173,41 +173,59 @@ class ResKVLayerCache(_LayerBase):
             self.keys[:, :, self.live: self.live + 1].copy_(key_states)
             self.raw_keys[:, :, self.live: self.live + 1].copy_(raw)
             self.values[:, :, self.live: self.live + 1].copy_(value_states)
-            self.live += 1
-            if self.live == self.keys.shape[2]:
-                k_grp = self.raw_keys[:, :, :group].contiguous()
-                v_grp = self.values[:, :, :group].contiguous()
-                if self._k is None:
-                    self._store(compress(k_grp, v_grp, self.config, plan=self.plan), extra=16 * group)
-                else:
-                    k, v = _compress_group(k_grp, v_grp, self.config, self.compressed, self.plan)
-                    self._k.append(k)
-                    self._v.append(v)
-                    self._view = None
-                remain = self.live - group
-                for buf in (self.keys, self.raw_keys, self.values):
-                    buf[:, :, :remain].copy_(buf[:, :, group: self.live].clone())
-                self.live = remain
+            self._take_token()
+            return self.keys[:, :, : self.live], self.values[:, :, : self.live]
         self.length += q_len
         return self.keys[:, :, : self.live], self.values[:, :, : self.live]
 
+    def advance(self):
+        """Accounts for one decode token that the caller has already written into
+        ring slot ``live`` of ``keys`` (rotated K), ``raw_keys`` (pre-RoPE K)
+        and ``values``, e.g. from a captured graph; otherwise the same as
+        ``update`` with that token (the ring is compressed by a group when full)."""
+        if not self.is_initialized or self.length == 0:
+            raise ValueError("advance() continues a prefilled cache")
+        self._take_token()
+
+    def _take_token(self):
+        """One more token in the ring; a full ring gives its oldest group to the compressed history."""
+        group = self.config.group_size
+        self.live += 1
+        self.length += 1
+        if self.live < self.keys.shape[2]:
+            return
+        k_grp = self.raw_keys[:, :, :group].contiguous()
+        v_grp = self.values[:, :, :group].contiguous()
+        if self._k is None:
+            self._store(compress(k_grp, v_grp, self.config, plan=self.plan), extra=16 * group)
+        else:
+            k, v = _compress_group(k_grp, v_grp, self.config, self.compressed, self.plan)
+            self._k.append(k)
+            self._v.append(v)
+            self._view = None
+        remain = self.live - group
+        for buf in (self.keys, self.raw_keys, self.values):
+            buf[:, :, :remain].copy_(buf[:, :, group: self.live].clone())
+        self.live = remain
+
     # -- decode attention (reskv/models/llama.py:45-60) ------------------------
-    def attend(self, query, query_rot, *, scaling, inv_freq=None, rope_theta=500000.0):
+    def attend(self, query, query_rot, *, scaling, inv_freq=None, rope_theta=500000.0, out=None):
         """Attention of the newest token (after ``update``) over the compressed
         history and the dense ring, as the model patch computes it with
         ``attention(query, self.compressed, position=self.length - 1,
         recent=(query_rot, ring K, ring V))``.  Repeated steps reuse the
         descriptors, RoPE table and buffers until a group compression changes
         the history; the ring is read in place.  query / query_rot fp16
-        [B, Hq, 1, 128] (pre-RoPE / rotated, contiguous).  The returned tensor
-        is reused by the next call."""
+        [B, Hq, 1, 128] (pre-RoPE / rotated, contiguous).  The result goes to
+        ``out`` (contiguous fp16, B * Hq * 128 elements) when given; otherwise
+        the returned tensor is reused by the next call."""
         cv = self.compressed
         if cv is None:
             raise ValueError("no compressed history yet; attend over the ring densely")
         if self._stepper is None or self._stepper.cache is not cv:
             self._stepper = StepDecoder(cv, query.shape[1], scaling, inv_freq, rope_theta)
         return self._stepper.run(query, self.length - 1, query_rot, self.keys, self.values, self.live,
-                                 self.keys.shape[2])
+                                 self.keys.shape[2], out=out)
 
     # -- queries -------------------------------------------------------------
     def get_seq_length(self, *_):

@@ -882,17 +882,118 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
 constexpr int kMergeThreads = 256;
 constexpr int kMergeRegD = 8;  // residual-sum splits per thread held in registers
 constexpr int kMergeRegB = 4;  // cluster-mass splits per thread held in registers
+constexpr int kRecentThreads = 128;  // recent tokens per chunk of the joint softmax
 
+// Dense recent tokens joined to a compressed result (Tr may be 0).
+struct RecentArgs {
+    const uint16_t* q_rope;  // fp16 [B*Hq, 128], rotated query
+    const uint16_t* k;       // fp16 rotated keys, rows of rs tokens per (batch, KV head)
+    const uint16_t* v;       // fp16 values, same layout
+    int Tr, rs;
+    float scaling;
+};
+
+// Block max / sum over the NT / 64 waves of an NT-thread workgroup (NT = 128
+// or 256).
+template <int NT>
+__device__ __forceinline__ float block_max_nt(float v, float* red) {
+    v = wave_max(v);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    v = NT == 128 ? fmaxf(red[0], red[1]) : fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    __syncthreads();
+    return v;
+}
+template <int NT>
+__device__ __forceinline__ float block_sum_nt(float v, float* red) {
+    v = wave_sum(v);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    v = NT == 128 ? red[0] + red[1] : (red[0] + red[1]) + (red[2] + red[3]);
+    __syncthreads();
+    return v;
+}
+
+// Joint softmax (natural-log units) of the compressed result of row bq --
+// channel value oc of thread tid < 128, maximum cm, normaliser cl -- with its
+// Tr recent tokens, by an NT-thread workgroup.  The tokens are taken in chunks
+// of 128: threads 0..127 score token c0 + tid (given fp32 scores, or a
+// 128-dim dot product with the scaled rotated query) and own channel tid of
+// the weighted value sum; chunks combine by online rescaling.  Every sum is
+// written as an explicit FMA or rounded product, so the merge_recent kernel
+// and the fused split merge, which both call this, agree bit for bit.
+template <int NT>
+__device__ float recent_join(float oc, float cm, float cl, const RecentArgs& r, const float* scores, long bq,
+                             long bh, float* s_q, float* s_p, float* s_red) {
+#pragma clang fp contract(off)
+    const int tid = threadIdx.x;
+    const bool row = tid < kRecentThreads;
+    if (scores == nullptr && tid < kDim) s_q[tid] = h2f(r.q_rope[bq * kDim + tid]) * r.scaling;
+    __syncthreads();
+    float m = -INFINITY, l = 0.0f, acc = 0.0f;  // acc: channel tid
+    for (int c0 = 0; c0 < r.Tr; c0 += kRecentThreads) {
+        const int t = c0 + tid;
+        const bool live = row && t < r.Tr;
+        float s = -INFINITY;
+        if (live) {
+            if (scores != nullptr) {
+                s = scores[bq * r.Tr + t];
+            } else {
+                const uint4* kr = reinterpret_cast<const uint4*>(r.k + (bh * r.rs + t) * kDim);
+                float d = 0.0f;
+#pragma unroll
+                for (int i = 0; i < kDim / 8; ++i) {
+                    const uint4 w = kr[i];
+                    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        d = fmaf(s_q[8 * i + 2 * j], h2f((uint16_t)(ws[j] & 0xFFFFu)), d);
+                        d = fmaf(s_q[8 * i + 2 * j + 1], h2f((uint16_t)(ws[j] >> 16)), d);
+                    }
+                }
+                s = d;
+            }
+        }
+        const float mn = fmaxf(m, block_max_nt<NT>(s, s_red));
+        const float p = live ? expf(s - mn) : 0.0f;
+        if (row) s_p[tid] = p;
+        const float ps = block_sum_nt<NT>(p, s_red);  // its barriers also publish s_p
+        const float alpha = expf(m - mn);  // 0 for the first chunk (m = -inf, mn finite)
+        l = fmaf(l, alpha, ps);
+        if (tid < kDim) {
+            const int n = min(kRecentThreads, r.Tr - c0);
+            const uint16_t* vr = r.v + (bh * r.rs + c0) * kDim + tid;
+            float a = 0.0f;
+            for (int j = 0; j < n; ++j) a = fmaf(s_p[j], h2f(vr[(long)j * kDim]), a);
+            acc = fmaf(acc, alpha, a);
+        }
+        m = mn;
+        __syncthreads();  // s_p reads done before the next chunk writes it
+    }
+    const float jm = fmaxf(cm, m);
+    const float wc = cl > 0.0f ? __fmul_rn(cl, expf(cm - jm)) : 0.0f;
+    const float wr = r.Tr > 0 ? expf(m - jm) : 0.0f;
+    const float denom = fmaf(l, wr, wc);
+    const float inv = denom > 0.0f ? 1.0f / denom : 0.0f;
+    return __fmul_rn(fmaf(oc, wc, __fmul_rn(acc, wr)), inv);
+}
+
+// RECENT: the compressed result, rounded to fp16 as the unfused path stores
+// it, is joined with the recent tokens of `rc` before it is written.
+template <bool RECENT>
 __global__ void __launch_bounds__(kMergeThreads) decode_merge_kernel(
     const float* __restrict__ pm, const float* __restrict__ pl, const float* __restrict__ pdelta,
     const float* __restrict__ pbeta, const uint16_t* __restrict__ vcent, int vnc, int vcs, int Hq, int H,
-    int splits, uint16_t* __restrict__ out, float* __restrict__ om, float* __restrict__ ol) {
+    int splits, uint16_t* __restrict__ out, float* __restrict__ om, float* __restrict__ ol, RecentArgs rc) {
+#pragma clang fp contract(off)  // every product and sum as written (FMAs are explicit)
     __shared__ float s_w[kMaxSplits];
     __shared__ float s_red[kMergeThreads / kWave];
     __shared__ float4 s_d[8][kDim / 4];
     __shared__ float4 s_b[16][kMaxClusters / 4];
     __shared__ float s_beta[kMaxClusters];
     __shared__ uint4 s_vc[kMaxClusters * kDim / 8];  // fp16 Value centroids [c][128]
+    __shared__ float s_q[RECENT ? kDim : 1];
+    __shared__ float s_p[RECENT ? kRecentThreads : 1];
     const long bq = blockIdx.x;  // b * Hq + hq
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int G = Hq / H;
@@ -945,14 +1046,14 @@ __global__ void __launch_bounds__(kMergeThreads) decode_merge_kernel(
         if (tid < splits) {
             const float w = l0 > 0.0f ? exp2_fast(m0 - mx) : 0.0f;
             s_w[tid] = w;
-            lsum = l0 * w;
+            lsum = __fmul_rn(l0, w);
         }
     } else {
         for (int sp = tid; sp < splits; sp += kMergeThreads) {
             const float lw = l_row[sp];
             const float w = lw > 0.0f ? exp2_fast(m_row[sp] - mx) : 0.0f;
             s_w[sp] = w;
-            lsum += lw * w;
+            lsum = fmaf(lw, w, lsum);
         }
     }
     lsum = wave_sum(lsum);
@@ -1013,6 +1114,7 @@ __global__ void __launch_bounds__(kMergeThreads) decode_merge_kernel(
     }
     __syncthreads();
     // 5) fold sum_c beta_c c_v[c], normalise (threads 0..127: one channel each)
+    uint16_t oc = 0;
     if (tid < kDim) {
         const float* sd = reinterpret_cast<const float*>(s_d);
         float acc = 0.0f;
@@ -1023,99 +1125,47 @@ __global__ void __launch_bounds__(kMergeThreads) decode_merge_kernel(
             for (int c = 0; c < vnc; ++c) acc = fmaf(s_beta[c], h2f(vc[c * kDim]), acc);
         }
         const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
-        out[bq * kDim + tid] = f2h(acc * inv);
-        if (tid == 0) {
-            if (om) om[bq] = mx * kLn2;  // natural-log units, as the reference returns m
-            if (ol) ol[bq] = lsum;
+        oc = f2h(acc * inv);
+        if constexpr (!RECENT) {
+            out[bq * kDim + tid] = oc;
+            if (tid == 0) {
+                if (om) om[bq] = __fmul_rn(mx, kLn2);  // natural-log units, as the reference returns m
+                if (ol) ol[bq] = lsum;
+            }
         }
+    }
+    if constexpr (RECENT) {
+        // the same rounded product as the m the unfused merge stores (no contraction into cm - jm)
+        const float r = recent_join<kMergeThreads>(h2f(oc), __fmul_rn(mx, kLn2), lsum, rc, nullptr, bq, bh, s_q, s_p,
+                                                   s_red);
+        if (tid < kDim) out[bq * kDim + tid] = f2h(r);
     }
 }
 
 // Joint softmax of a normalised compressed result (m, l) with Tr recent tokens
-// whose scaled scores are given (scores != null) or computed from q_rope/k.
-// Recent K/V rows of (batch, head) block bh start at token bh * rs.
-// One 128-thread workgroup per (batch, query head): the window is taken in
-// chunks of 128 tokens, thread t scoring token t of the chunk (a full 128-dim
-// dot product against the query in LDS) and then owning channel t of the
-// weighted value sum; chunks combine by online rescaling (natural-log units).
-constexpr int kRecentThreads = 128;
-
-__device__ __forceinline__ float block_max128(float v, float* red) {
-    v = wave_max(v);
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-    __syncthreads();
-    v = fmaxf(red[0], red[1]);
-    __syncthreads();
-    return v;
-}
-__device__ __forceinline__ float block_sum128(float v, float* red) {
-    v = wave_sum(v);
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-    __syncthreads();
-    v = red[0] + red[1];
-    __syncthreads();
-    return v;
-}
-
-__global__ void __launch_bounds__(kRecentThreads) merge_recent_kernel(
+// whose scaled scores are given (scores != null) or computed from q_rope/k
+// (recent_join).  Recent K/V rows of (batch, head) block bh start at token
+// bh * rs.  One workgroup per (batch, query head), of the split merge's 256
+// threads: both kernels then run the same code for the join (the upper 128
+// threads take part in its reductions only).
+__global__ void __launch_bounds__(kMergeThreads) merge_recent_kernel(
     const uint16_t* __restrict__ comp_out, const float* __restrict__ comp_m, const float* __restrict__ comp_l,
     const float* __restrict__ scores, const uint16_t* __restrict__ q_rope, const uint16_t* __restrict__ k_recent,
     const uint16_t* __restrict__ v_recent, int Hq, int H, int Tr, int rs, float scaling,
     uint16_t* __restrict__ out) {
+#pragma clang fp contract(off)
     __shared__ float s_q[kDim];
     __shared__ float s_p[kRecentThreads];
-    __shared__ float s_red[kRecentThreads / kWave];
+    __shared__ float s_red[kMergeThreads / kWave];
     const long bq = blockIdx.x;
     const int tid = threadIdx.x;
     const int G = Hq / H;
     const long b = bq / Hq, hq = bq % Hq;
     const long bh = b * H + hq / G;
-    if (scores == nullptr) s_q[tid] = h2f(q_rope[bq * kDim + tid]) * scaling;
-    __syncthreads();
-    float m = -INFINITY, l = 0.0f, acc = 0.0f;  // acc: channel tid
-    for (int c0 = 0; c0 < Tr; c0 += kRecentThreads) {
-        const int t = c0 + tid;
-        float s = -INFINITY;
-        if (t < Tr) {
-            if (scores != nullptr) {
-                s = scores[bq * Tr + t];
-            } else {
-                const uint4* kr = reinterpret_cast<const uint4*>(k_recent + (bh * rs + t) * kDim);
-                float d = 0.0f;
-#pragma unroll
-                for (int i = 0; i < kDim / 8; ++i) {
-                    const uint4 w = kr[i];
-                    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        d = fmaf(s_q[8 * i + 2 * j], h2f((uint16_t)(ws[j] & 0xFFFFu)), d);
-                        d = fmaf(s_q[8 * i + 2 * j + 1], h2f((uint16_t)(ws[j] >> 16)), d);
-                    }
-                }
-                s = d;
-            }
-        }
-        const float mn = fmaxf(m, block_max128(s, s_red));
-        const float p = t < Tr ? expf(s - mn) : 0.0f;
-        s_p[tid] = p;
-        const float ps = block_sum128(p, s_red);  // its barriers also publish s_p
-        const float alpha = expf(m - mn);  // 0 for the first chunk (m = -inf, mn finite)
-        l = l * alpha + ps;
-        const int n = min(kRecentThreads, Tr - c0);
-        const uint16_t* vr = v_recent + (bh * rs + c0) * kDim + tid;
-        float a = 0.0f;
-        for (int j = 0; j < n; ++j) a = fmaf(s_p[j], h2f(vr[(long)j * kDim]), a);
-        acc = acc * alpha + a;
-        m = mn;
-        __syncthreads();  // s_p reads done before the next chunk writes it
-    }
-    const float cm = comp_m[bq], cl = comp_l[bq];
-    const float jm = fmaxf(cm, m);
-    const float wc = cl > 0.0f ? cl * expf(cm - jm) : 0.0f;
-    const float wr = Tr > 0 ? expf(m - jm) : 0.0f;
-    const float denom = wc + l * wr;
-    const float inv = denom > 0.0f ? 1.0f / denom : 0.0f;
-    out[bq * kDim + tid] = f2h((h2f(comp_out[bq * kDim + tid]) * wc + acc * wr) * inv);
+    const RecentArgs r{q_rope, k_recent, v_recent, Tr, rs, scaling};
+    const float oc = tid < kDim ? h2f(comp_out[bq * kDim + tid]) : 0.0f;
+    const float res = recent_join<kMergeThreads>(oc, comp_m[bq], comp_l[bq], r, scores, bq, bh, s_q, s_p, s_red);
+    if (tid < kDim) out[bq * kDim + tid] = f2h(res);
 }
 
 // ---------------------------------------------------------------------------
@@ -1266,7 +1316,8 @@ int launch_partial(int kf, int vf, int G, dim3 grid, size_t shm, hipStream_t st,
 
 int run_decode(const void* q, int kf, const DTensor& k, int vf, const DTensor& v, const float* inv_freq,
                const float* rope, int B, int Hq, int H, int T, int start_pos, int pos_q, float scaling, int splits,
-               void* out, float* m, float* l, void* ws, int64_t ws_bytes, void* stream) {
+               void* out, float* m, float* l, void* ws, int64_t ws_bytes, void* stream,
+               const RecentArgs* recent = nullptr) {
     RESKV_REQUIRE(q && inv_freq && out, "null pointer argument");
     RESKV_REQUIRE(B > 0 && H > 0 && T > 0, "batch, head and token counts must be positive");
     RESKV_REQUIRE(Hq % H == 0, "query heads must be a multiple of KV heads");
@@ -1307,8 +1358,15 @@ int run_decode(const void* q, int kf, const DTensor& k, int vf, const DTensor& v
     p.pb = p.pd + (long)B * Hq * S * kDim;
     hipStream_t st = (hipStream_t)stream;
     if (launch_partial(kf, vf, G, dim3(S, H, B), shm, st, p)) return 1;
-    hipLaunchKernelGGL(decode_merge_kernel, dim3(B * Hq), dim3(kMergeThreads), 0, st, p.pm, p.pl, p.pd, p.pb,
-                       cent ? v.cent : nullptr, v.nc, v.cs, Hq, H, S, (uint16_t*)out, m, l);
+    if (recent != nullptr) {
+        hipLaunchKernelGGL(decode_merge_kernel<true>, dim3(B * Hq), dim3(kMergeThreads), 0, st, p.pm, p.pl, p.pd,
+                           p.pb, cent ? v.cent : nullptr, v.nc, v.cs, Hq, H, S, (uint16_t*)out, nullptr, nullptr,
+                           *recent);
+    } else {
+        hipLaunchKernelGGL(decode_merge_kernel<false>, dim3(B * Hq), dim3(kMergeThreads), 0, st, p.pm, p.pl, p.pd,
+                           p.pb, cent ? v.cent : nullptr, v.nc, v.cs, Hq, H, S, (uint16_t*)out, m, l,
+                           RecentArgs{});
+    }
     return reskv_host::check_launch("decode_merge_kernel");
 }
 
@@ -1337,6 +1395,27 @@ extern "C" int reskv_decode_rope(const void* q, const reskv_ctensor* k, const re
     const int kf = dfmt_of(k), vf = dfmt_of(v);
     return run_decode(q, kf, to_dt(k, kf, T), vf, to_dt(v, vf, T), inv_freq, rope_table, B, Hq, H, T, start_pos,
                       pos_q, scaling, splits, out, m, l, workspace, workspace_bytes, stream);
+}
+
+extern "C" int reskv_decode_recent(const void* q, const reskv_ctensor* k, const reskv_ctensor* v,
+                                   const float* inv_freq, const float* rope_table, int B, int Hq, int H, int T,
+                                   int start_pos, int pos_q, float scaling, int splits, const void* q_rope,
+                                   const void* k_recent, const void* v_recent, int Tr, int r_stride, void* out,
+                                   void* workspace, int64_t workspace_bytes, void* stream) {
+    if (check_ct(k, "K") || check_ct(v, "V")) return 1;
+    RESKV_REQUIRE((k->t_stride == 0 || k->t_stride >= T) && (v->t_stride == 0 || v->t_stride >= T),
+                  "token row stride must be 0 or at least T");
+    RESKV_REQUIRE((k->c_stride == 0 || k->c_stride >= k->nc) && (v->c_stride == 0 || v->c_stride >= v->nc),
+                  "centroid row stride must be 0 or at least nc");
+    RESKV_REQUIRE(Tr >= 0, "bad recent-merge sizes");
+    const int rs = r_stride > 0 ? r_stride : Tr;
+    RESKV_REQUIRE(rs >= Tr, "recent row stride shorter than the window");
+    RESKV_REQUIRE(Tr == 0 || (q_rope && k_recent && v_recent), "null recent tensors");
+    RESKV_REQUIRE(Tr == 0 || ((((uintptr_t)k_recent) & 15u) == 0), "recent K must be 16-byte aligned");
+    const RecentArgs rc{(const uint16_t*)q_rope, (const uint16_t*)k_recent, (const uint16_t*)v_recent, Tr, rs, scaling};
+    const int kf = dfmt_of(k), vf = dfmt_of(v);
+    return run_decode(q, kf, to_dt(k, kf, T), vf, to_dt(v, vf, T), inv_freq, rope_table, B, Hq, H, T, start_pos,
+                      pos_q, scaling, splits, out, nullptr, nullptr, workspace, workspace_bytes, stream, &rc);
 }
 
 extern "C" int reskv_decode(const void* q, const reskv_ctensor* k, const reskv_ctensor* v,
@@ -1391,7 +1470,7 @@ extern "C" int reskv_merge_recent_scores(const void* comp_out, const float* comp
     RESKV_REQUIRE(comp_out && comp_m && comp_l && out, "null pointer argument");
     RESKV_REQUIRE(B > 0 && H > 0 && Hq % H == 0 && Tr >= 0, "bad recent-merge sizes");
     RESKV_REQUIRE(Tr == 0 || (scores && v_recent), "null recent scores/values");
-    hipLaunchKernelGGL(merge_recent_kernel, dim3(B * Hq), dim3(kRecentThreads), 0, (hipStream_t)stream,
+    hipLaunchKernelGGL(merge_recent_kernel, dim3(B * Hq), dim3(kMergeThreads), 0, (hipStream_t)stream,
                        (const uint16_t*)comp_out, comp_m, comp_l, scores, nullptr, nullptr,
                        (const uint16_t*)v_recent, Hq, H, Tr, Tr, 1.0f, (uint16_t*)out);
     return reskv_host::check_launch("merge_recent_kernel");
@@ -1407,7 +1486,7 @@ extern "C" int reskv_merge_recent_qk(const void* comp_out, const float* comp_m, 
     RESKV_REQUIRE(rs >= Tr, "recent row stride shorter than the window");
     RESKV_REQUIRE(Tr == 0 || (q_rope && k_recent && v_recent), "null recent tensors");
     RESKV_REQUIRE(Tr == 0 || ((((uintptr_t)k_recent) & 15u) == 0), "recent K must be 16-byte aligned");
-    hipLaunchKernelGGL(merge_recent_kernel, dim3(B * Hq), dim3(kRecentThreads), 0, (hipStream_t)stream,
+    hipLaunchKernelGGL(merge_recent_kernel, dim3(B * Hq), dim3(kMergeThreads), 0, (hipStream_t)stream,
                        (const uint16_t*)comp_out, comp_m, comp_l, nullptr, (const uint16_t*)q_rope,
                        (const uint16_t*)k_recent, (const uint16_t*)v_recent, Hq, H, Tr, rs, scaling, (uint16_t*)out);
     return reskv_host::check_launch("merge_recent_kernel");

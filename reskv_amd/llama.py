@@ -1,12 +1,16 @@
 """Random-init Llama-3.1-8B-shaped decoder for the end-to-end decode benchmark.
 
 The decode branch follows the reference model patch
-(reskv/models/llama.py:36-72): each layer hands the new token's rotated K, V
-and pre-RoPE ("raw") K to ``ResKVLayerCache.update`` and attends with the
+(reskv/models/llama.py:36-72): each layer adds the new token's rotated K, V
+and pre-RoPE ("raw") K to its ``ResKVLayerCache`` and attends with the
 pre-RoPE query against the compressed history, merging the dense ring
-(rotated Q/K and V) as the recent window.  The dense baseline keeps pre-RoPE
-K and V in a preallocated fp16 cache and runs the same split-K engine over it
+(rotated Q/K and V) as the recent window.  The token is written into the ring
+by the layer's captured graph (slot from device memory) and the cache then
+accounts for it (``advance``), which is ``update`` without its copies.  The
+dense baseline keeps pre-RoPE K and V in a preallocated fp16 cache, appended
+the same way, and runs the same split-K engine over it
 (``reskv_decode_dense``, which rotates K in-kernel like the compressed path).
+Both write the attention output straight into the buffer the next graph reads.
 
 No checkpoint can be fetched, so the weights are random (N(0, 0.02), unit
 RMSNorm gains).  Around attention the work has fixed shapes -- RMSNorm, the
@@ -187,6 +191,7 @@ class GreedyDecoder:
         self.attn = torch.zeros(batch, s.heads, s.head_dim, **f16)
         self.tok = torch.zeros(batch, dtype=torch.int64, device=dev)
         self.pos_buf = torch.zeros(1, dtype=torch.int64, device=dev)
+        self.slot_buf = torch.zeros(1, dtype=torch.int64, device=dev)  # ring slot of the new token
         if mode == "reskv":
             cfg = kernel_config or ResKVKernelConfig(sparsity=0.75)
             self.caches = [ResKVLayerCache(cfg) for _ in range(s.layers)]
@@ -211,7 +216,7 @@ class GreedyDecoder:
         self.x.copy_(self.model.embed[self.tok])
 
     # -- fixed-shape parts as graphs -----------------------------------------
-    def _pre(self, p):
+    def _pre(self, li, p):
         s = self.model.shape
         h = _rmsnorm(self.x, p["n1"], s.rms_eps)
         q, k, v = self._split_step(F.linear(h, p["wqkv"]))
@@ -222,6 +227,25 @@ class GreedyDecoder:
         self.v.copy_(v)
         self.qr.copy_(_rotate(q, cos, sin))
         self.kr.copy_(_rotate(k, cos, sin))
+        self._append(li)
+
+    def _append(self, li):
+        """The new token's K/V into layer li's cache, at a slot read from device
+        memory (inside the pre graph, so the append costs no launches of its own)."""
+        if self.mode == "reskv":
+            layer = self.caches[li]
+            layer.keys.index_copy_(2, self.slot_buf, self.kr[:, :, None])
+            layer.raw_keys.index_copy_(2, self.slot_buf, self.k[:, :, None])
+            layer.values.index_copy_(2, self.slot_buf, self.v[:, :, None])
+        else:
+            self.kc[li].index_copy_(2, self.pos_buf, self.k[:, :, None])
+            self.vc[li].index_copy_(2, self.pos_buf, self.v[:, :, None])
+
+    def _set_slots(self):
+        """Device copies of this step's position and ring slot (the layers' rings fill in step)."""
+        self.pos_buf.fill_(self.pos)
+        if self.mode == "reskv":
+            self.slot_buf.fill_(self.caches[0].live)
 
     def _split_step(self, qkv):
         return self.model._split(qkv)
@@ -241,22 +265,25 @@ class GreedyDecoder:
         self.x.copy_(self.model.embed.index_select(0, self.tok))
 
     def capture(self):
-        """Records the fixed-shape parts once (after a warm-up on a side stream)."""
+        """Records the fixed-shape parts once (after a warm-up on a side stream).
+        The warm-up appends layer 0's token at this step's slot, which the
+        step's own append then overwrites with the same values."""
+        self._set_slots()
         x0, tok0 = self.x.clone(), self.tok.clone()
         side = torch.cuda.Stream(device=self.model.device)
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side):
             for p in self.model.layers[:1]:
-                self._pre(p)
+                self._pre(0, p)
                 self._post(p)
             self._head()
         torch.cuda.current_stream().wait_stream(side)
         pool = torch.cuda.graph_pool_handle()
         pre, post = [], []
-        for p in self.model.layers:
+        for li, p in enumerate(self.model.layers):
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g, pool=pool):
-                self._pre(p)
+                self._pre(li, p)
             pre.append(g)
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g, pool=pool):
@@ -271,29 +298,26 @@ class GreedyDecoder:
 
     # -- attention ---------------------------------------------------------------
     def _attend(self, li):
-        b = self.batch
+        # the pre graph has already written the token's K/V into the cache
         if self.mode == "reskv":
             layer = self.caches[li]
-            layer.update(self.kr[:, :, None], self.v[:, :, None], {"raw_keys": self.k[:, :, None]})
-            out = layer.attend(self.q[:, :, None], self.qr[:, :, None], scaling=self.model.scaling,
-                               inv_freq=self.model.inv_freq)
+            layer.advance()
+            layer.attend(self.q[:, :, None], self.qr[:, :, None], scaling=self.model.scaling,
+                         inv_freq=self.model.inv_freq, out=self.attn)
         else:
             t = self.pos + 1
-            self.kc[li][:, :, self.pos].copy_(self.k)
-            self.vc[li][:, :, self.pos].copy_(self.v)
-            out = dense_decode(self.q[:, :, None], self.kc[li][:, :, :t], self.vc[li][:, :, :t],
-                               self.model.inv_freq, position=self.pos, scaling=self.model.scaling)
-        self.attn.copy_(out.view(b, -1, self.model.shape.head_dim))
+            dense_decode(self.q[:, :, None], self.kc[li][:, :, :t], self.vc[li][:, :, :t], self.model.inv_freq,
+                         position=self.pos, scaling=self.model.scaling, out=self.attn)
 
     def step(self, events=None):
         """One decode step for every sequence; returns the new tokens [B] (device).
         ``events`` (list) collects (before, after) CUDA events around each attention."""
-        if self.graphs is None:
-            self.capture()
         if self.pos >= self.max_pos:
             raise RuntimeError("decoder capacity exhausted")
+        if self.graphs is None:
+            self.capture()
+        self._set_slots()
         pre, post, head = self.graphs
-        self.pos_buf.fill_(self.pos)
         for li in range(len(pre)):
             pre[li].replay()
             if events is not None:

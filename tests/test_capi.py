@@ -22,7 +22,8 @@ def test_header_declares_the_operator_surface():
     for required in ("reskv_compress_fp16", "reskv_compress_bitmap", "reskv_compress_quantized",
                      "reskv_compress_structured_int4", "reskv_kmeans", "reskv_kmeans_assign", "reskv_kmeans_kv",
                      "reskv_decode",
-                     "reskv_merge_recent_scores", "reskv_merge_recent_qk", "reskv_decode_dense"):
+                     "reskv_merge_recent_scores", "reskv_merge_recent_qk", "reskv_decode_recent",
+                     "reskv_decode_dense"):
         assert required in names
 
 
@@ -47,6 +48,8 @@ def test_null_pointers_are_rejected_without_a_gpu():
     assert "null" in _err(lib.reskv_kmeans_kv(*([None] * 8), 1, 1, 1, 1, None, 0, None))
     assert "null" in _err(lib.reskv_merge_recent_qk(None, None, None, None, None, None, 1, 4, 1, 1, 0, 1.0, None,
                                                     None))
+    assert "null" in _err(lib.reskv_decode_recent(None, None, None, None, None, 1, 4, 1, 16, 0, 15, 1.0, 0, None,
+                                                  None, None, 1, 0, None, None, 0, None))
 
 
 @pytest.mark.parametrize(

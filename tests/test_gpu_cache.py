@@ -118,3 +118,31 @@ def test_attend_fast_path_equals_attention(device, bits, sparsity):
         ref = attention(q, layer.compressed, position=layer.length - 1, inv_freq=freq, scaling=0.1,
                         recent=(qr, layer.keys[:, :, :layer.live], layer.values[:, :, :layer.live]))
         assert torch.equal(fast, ref), t
+
+
+@pytest.mark.parametrize("sparsity,ring_len", [(0.5, 0), (0.5, 96), (0.75, 200)])
+def test_step_decoder_one_merge_launch_equals_two(device, sparsity, ring_len):
+    """reskv_decode_recent (the recent window joined inside the split merge) is bitwise
+    decode + reskv_merge_recent_qk, including windows of more than one 128-token chunk,
+    row-strided ring buffers and a caller-provided output buffer."""
+    from reskv_amd._extension import StepDecoder
+
+    k, v = _inputs(512, device, seed=21, b=2, h=2)
+    cache = compress(k, v, ResKVKernelConfig(sparsity=sparsity, num_clusters=8))
+    g = seeded(22)
+    stride = max(ring_len, 1) + 8
+    ring_k = (torch.randn(2, 2, stride, 128, generator=g) * 0.5).half().to(device)
+    ring_v = (torch.randn(2, 2, stride, 128, generator=g) * 0.5).half().to(device)
+    q = torch.randn(2, 8, 1, 128, generator=g).half().to(device)
+    qr = torch.randn(2, 8, 1, 128, generator=g).half().to(device)
+    freq = (500000.0 ** (-torch.arange(64).float() / 64)).to(device)
+    step = StepDecoder(cache, 8, 0.1, freq)
+    out = torch.full((2, 8, 1, 128), float("nan"), dtype=torch.float16, device=device)
+    pos = 512 + ring_len
+    got = step.run(q, pos, qr, ring_k, ring_v, ring_len, stride, out=out)
+    assert got.data_ptr() == out.data_ptr()
+    recent = None if ring_len == 0 else (qr, ring_k[:, :, :ring_len], ring_v[:, :, :ring_len])
+    ref = attention(q, cache, position=pos, inv_freq=freq, scaling=0.1, recent=recent)
+    assert torch.equal(out, ref)
+    again = step.run(q, pos, qr, ring_k, ring_v, ring_len, stride)
+    assert torch.equal(again, ref)

@@ -4,16 +4,39 @@ import pytest
 import torch
 
 from reskv_amd import ResKVKernelConfig
+from reskv_amd._extension import dense_decode
 from reskv_amd.llama import GreedyDecoder, LlamaShape, RandomLlama, llama3_inv_freq
 
 TINY = LlamaShape(layers=2, hidden=512, heads=4, kv_heads=1, ffn=1024, vocab=1000)
 
 
-def _run(mode, steps=70, prompt=256, batch=2):
+class _EagerAppend(GreedyDecoder):
+    """The harness with the K/V append outside the graphs, through the cache's own
+    ``update`` (ResKV) or slice copies (dense), and the output copied."""
+
+    def _append(self, li):
+        pass
+
+    def _attend(self, li):
+        if self.mode == "reskv":
+            layer = self.caches[li]
+            layer.update(self.kr[:, :, None], self.v[:, :, None], {"raw_keys": self.k[:, :, None]})
+            out = layer.attend(self.q[:, :, None], self.qr[:, :, None], scaling=self.model.scaling,
+                               inv_freq=self.model.inv_freq)
+        else:
+            t = self.pos + 1
+            self.kc[li][:, :, self.pos].copy_(self.k)
+            self.vc[li][:, :, self.pos].copy_(self.v)
+            out = dense_decode(self.q[:, :, None], self.kc[li][:, :, :t], self.vc[li][:, :, :t],
+                               self.model.inv_freq, position=self.pos, scaling=self.model.scaling)
+        self.attn.copy_(out.view(self.batch, -1, self.model.shape.head_dim))
+
+
+def _run(mode, steps=70, prompt=256, batch=2, cls=GreedyDecoder):
     model = RandomLlama(TINY, "cuda", seed=1)
     ids = torch.randint(128, TINY.vocab, (batch, prompt), generator=torch.Generator().manual_seed(3)).cuda()
     cfg = ResKVKernelConfig(sparsity=0.75, num_clusters=8, kmeans_iterations=4)
-    dec = GreedyDecoder(model, batch, prompt, steps, mode, cfg)
+    dec = cls(model, batch, prompt, steps, mode, cfg)
     keep = {}
 
     def sink(layer, raw_k, rot_k, v):
@@ -49,6 +72,24 @@ def test_decode_runs_and_keeps_cache_consistent(device, mode):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("mode", ["reskv", "dense"])
+def test_in_graph_append_equals_eager_update(device, mode):
+    """Appending inside the captured graphs (slot from device memory) and writing the
+    attention into the graph's buffer give bitwise the decode of the eager path, across
+    a group compression (the 96-slot ring, 64 tokens after the prompt, fills at step 32)."""
+    _, dec, _, toks = _run(mode)
+    _, ref, _, ref_toks = _run(mode, cls=_EagerAppend)
+    assert torch.equal(toks, ref_toks)
+    assert torch.equal(dec.x, ref.x)
+    if mode == "reskv":
+        for a, b in zip(dec.caches, ref.caches):
+            assert a.live == b.live and a.length == b.length
+            assert torch.equal(a.keys[:, :, :a.live], b.keys[:, :, :b.live])
+            assert torch.equal(a.values[:, :, :a.live], b.values[:, :, :b.live])
+            assert torch.equal(a.compressed.key.payload, b.compressed.key.payload)
+
+
+@pytest.mark.gpu
 def test_dense_first_step_attention_matches_fp32(device):
     """The harness's dense attention (strided cache, in-kernel RoPE) against fp32 attention."""
     model = RandomLlama(TINY, "cuda", seed=2)
@@ -57,7 +98,6 @@ def test_dense_first_step_attention_matches_fp32(device):
     first = model.prefill(ids, dec.absorb, q_rows=64)
     dec.start(first)
     dec.capture()
-    dec.pos_buf.fill_(dec.pos)
     dec.graphs[0][0].replay()
     dec._attend(0)
     t = dec.pos + 1
