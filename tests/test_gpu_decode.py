@@ -80,6 +80,45 @@ def test_gqa_and_64_centroids(device, ratio, bits, layout):
     assert _max_err(out, expected_attention(q, cache, position=330, start_position=10)) <= ATOL
 
 
+@pytest.mark.parametrize("fmt,width", [("bitmap", w) for w in (8, 16, 24, 32, 40, 64, 96, 128)] +
+                         [("tiled", w) for w in (8, 16, 32, 48, 64, 96)])
+def test_residual_widths_through_family_ops(device, fmt, width):
+    """Payload widths across the range the C ABI accepts, not only the plans'
+    32 and 64: widths above 64 take the wide decoders (four 16-byte pieces per
+    lane), widths 8 and 16 leave most lanes without a piece.  T = 300 leaves a
+    partial tile in every wave range."""
+    from reskv_amd._extension import load_extension
+
+    b, hk, g, t = 2, 2, 4, 300
+    k, v, q, ((kc, ki), (vc, vi)) = reference_test_inputs(b=b, t=t, heads=hk, gqa=g, seed=41)
+    comp = load_extension("compression")
+    if fmt == "bitmap":
+        enc = [comp.compress_bitmap(x, c, i, width) for x, c, i in ((k, kc, ki), (v, vc, vi))]
+    else:
+        enc = [comp.compress_fp16(x, c, i, width, False) for x, c, i in ((k, kc, ki), (v, vc, vi))]
+    (kp, km), (vp, vm) = enc
+    flat = lambda x: x.reshape(b * hk, *x.shape[2:]).contiguous()  # noqa: E731
+    ids8 = lambda x: flat(x).to(torch.int8)  # noqa: E731
+    freq = theta_freq()
+    scaling = 128 ** -0.5
+    args = (hk, hk * g, 7, 320, 500000.0, scaling)
+    Q = q.reshape(b * hk * g, 128).contiguous()
+    for splits in (0, 3):
+        if fmt == "bitmap":
+            out = load_extension("cluster_mass").decode_fp16(
+                Q, flat(kc), ids8(ki), flat(kp), flat(km), flat(vc), ids8(vi), flat(vp), flat(vm), *args,
+                False, splits, freq)[0]
+        else:
+            out = load_extension("attention", None).decode_fp16(
+                Q, flat(kc), ids8(ki), flat(kp), flat(km), None, flat(vc), ids8(vi), flat(vp), flat(vm), None,
+                *args, splits, freq)[0]
+        kd = o.reconstruct(fmt, np_(kc), np_(ki), np_(kp), np_(km))
+        vd = o.reconstruct(fmt, np_(vc), np_(vi), np_(vp), np_(vm))
+        ref = o.reference_attention(np_(q).astype(np.float64), kd, vd, position=320, start_position=7,
+                                    freq=np_(freq), scaling=scaling)
+        assert _max_err(out.view(b, hk * g, 1, 128), ref) <= ATOL, splits
+
+
 def test_structured_int4_large_logits(device):
     k, v, q, c = reference_test_inputs(t=256)
     k, q = k * 12, q * 12
