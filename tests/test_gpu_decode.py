@@ -119,6 +119,38 @@ def test_residual_widths_through_family_ops(device, fmt, width):
         assert _max_err(out.view(b, hk * g, 1, 128), ref) <= ATOL, splits
 
 
+@pytest.mark.parametrize("bits,sparsity,layout,b,t", [(16, 0.5, "unstructured", 32, 8192),
+                                                      (16, 0.75, "structured", 32, 8192),
+                                                      (4, 0.5, "unstructured", 8, 16384),
+                                                      (2, 0.5, "unstructured", 8, 16384)])
+def test_benchmark_shapes_against_fp32_checker(device, bits, sparsity, layout, b, t):
+    """Configs 2 and 3 at their full shapes (Hq = 32, Hk = 8): the split-K decode at the
+    automatic split count and at 16 splits against the float32 torch reconstruction
+    (reskv_amd.reference, pinned to the oracle's golden vectors on the CPU)."""
+    from reskv_amd.reference import reference_attention
+
+    g = torch.Generator(device=device).manual_seed(7)
+    shape = (b, 8, t, 128)
+    k = torch.randn(shape, device=device, dtype=torch.float16, generator=g) * 0.5
+    v = torch.randn(shape, device=device, dtype=torch.float16, generator=g) * 0.5
+    kc = torch.randn(b, 8, 32, 128, device=device, dtype=torch.float16, generator=g) * 0.1
+    vc = torch.randn(b, 8, 32, 128, device=device, dtype=torch.float16, generator=g) * 0.1
+    ki = torch.randint(32, shape[:3], device=device, dtype=torch.int32, generator=g)
+    vi = torch.randint(32, shape[:3], device=device, dtype=torch.int32, generator=g)
+    q = torch.randn(b, 32, 1, 128, device=device, dtype=torch.float16, generator=g)
+    cfg = ResKVKernelConfig(bits=bits, sparsity=sparsity, layout=layout)
+    cache = compress(k, v, cfg, clustering=((kc, ki), (vc, vi)))
+    del k, v
+    freq = theta_freq()
+    ref = reference_attention(q, cache, position=t, inv_freq=freq)
+    for splits in (0, 16):
+        out = attention(q, cache, position=t, inv_freq=freq, splits=splits)
+        err = (out.float() - ref).abs().max().item()
+        assert err <= ATOL, (splits, err)
+    del ref
+    torch.cuda.empty_cache()
+
+
 def test_structured_int4_large_logits(device):
     k, v, q, c = reference_test_inputs(t=256)
     k, q = k * 12, q * 12
