@@ -30,7 +30,7 @@ extern "C" {
 /* Thread-local description of the last failure; "" when none. */
 const char* reskv_last_error(void);
 
-/* Library ABI version (bumped on any signature or struct change); 2. */
+/* Library ABI version (bumped on any signature or struct change); 3. */
 int reskv_abi_version(void);
 
 /* ------------------------------------------------------------------ *
@@ -78,8 +78,10 @@ int64_t reskv_kmeans_workspace_bytes(int BH, int T, int C);
  * Replaces the torch loop of reskv/compression.py:37-53 (cdist, argmin,
  * one_hot, bmm).  x fp16 [BH,T,128]; centers_init fp32 [BH,C,128] (the
  * linspace-selected tokens); centers_out fp16 [BH,C,128]; ids int32 [BH,T]
- * (from the last assignment).  value_mode=0: K semantics (empty cluster keeps
- * its centre); 1: V semantics (empty cluster -> 0). */
+ * (from the last assignment).  value_mode=0: K semantics (fp32 distances,
+ * empty cluster keeps its centre); 1: V semantics (the fp16 cdist of
+ * compression.py:38 -- fp16 norms, fp16 distance, fp16 root, lowest index on
+ * ties -- fp16 centres, empty cluster -> 0). */
 int reskv_kmeans(const void* x, const float* centers_init, void* centers_out, int32_t* ids,
                  int BH, int T, int C, int iterations, int value_mode, void* workspace,
                  int64_t workspace_bytes, void* stream);
@@ -94,12 +96,14 @@ int reskv_kmeans_kv(const void* k, const void* v, const float* init_k, const flo
                     void* out_v, int32_t* ids_k, int32_t* ids_v, int BH, int T, int C, int iterations,
                     void* workspace, int64_t workspace_bytes, void* stream);
 
-/* Assignment step only: ids = argmin_c |x - c|^2 (lowest index on ties).
+/* Assignment step only: ids = argmin_c d(x, c) (lowest index on ties).
  * Replaces the assignment of reskv/compression.py:61-69 (_incremental_cluster,
- * one decode group against the shared centroid table).  centers fp32 [BH,C,128];
+ * one decode group against the shared centroid table).  centers fp32 [BH,C,128]
+ * (fp16 values for V).  value_mode=0: K, d = |x - c|^2 in fp32 (cdist, :66);
+ * 1: V, d = fp32(fp16(|x|^2 + |c|^2) - 2 x.c) with fp16 norms (:63-64).
  * workspace as for reskv_kmeans. */
 int reskv_kmeans_assign(const void* x, const float* centers, int32_t* ids, int BH, int T, int C,
-                        void* workspace, int64_t workspace_bytes, void* stream);
+                        int value_mode, void* workspace, int64_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------ *
  * Split-K fused decode attention over the compressed cache

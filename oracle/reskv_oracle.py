@@ -25,7 +25,12 @@ Restated functions and the reference lines they follow (under
 * ``kmeans``               -- compression.py:19-53 (Lloyd: linspace init,
                               assign-then-update, K keeps empty centres, V zeroes
                               them, ids from the last assignment)
-* ``incremental_cluster``  -- compression.py:56-69
+* ``value_distances``      -- compression.py:27, 38 (V: fp16 ``cdist`` in the mm
+                              formulation -- fp16 norms, one fp16 rounding of
+                              the 130-term sum, fp16 sqrt)
+* ``update_centres``       -- compression.py:40-52
+* ``incremental_cluster``  -- compression.py:56-69 (V: fp16(|x|^2 + |c|^2) - 2 x.c
+                              in fp32; group mean in fp16)
 
 How each function is pinned (tests/test_oracle.py):
 
@@ -34,20 +39,30 @@ How each function is pinned (tests/test_oracle.py):
 * packing: hand-computed words for known masks / codes (bit order MSB-first for
   bitmaps, LSB-first for tile masks, nibble and 2-bit positions);
 * quantisation: zero residual -> scale 1, all codes 0; codes bounded by QMAX;
-  decode(code) * scale reproduces the kept residual within half a step;
+  decode(code) * scale reproduces the kept residual within half a step; a
+  hand-computed multibit code that only the fp16-rounded scale gives;
 * reconstruct: encode -> reconstruct round trip equals centre + kept residual
   exactly, and the dropped channels are exactly the smallest |fp16(r)|;
 * attention: dense softmax closed form (one token -> output equals its value,
   equal scores -> mean), RoPE identities (relative-position invariance, norm
   preservation, inverse rotation);
-* k-means: ids are argmin of exact (float64) distances, centres are member
+* k-means, K: ids are argmin of exact (float64) distances, centres are member
   means, linspace initial indices, the constant-data known answer of
-  tests/test_cuda.py:161-169.
+  tests/test_cuda.py:161-169;
+* k-means, V: ``value_distances`` / ``assign_value`` against CPU torch's own
+  ``torch.cdist(..., compute_mode="use_mm_for_euclid_dist")`` on fp16 tensors
+  (equal fp16 distances and ids away from the tokens ``value_ambiguous``
+  flags); ``half_norms`` against ``x.pow(2).sum(-1)``; the incremental rule
+  against the reference's expression evaluated by CPU torch; the fp16 square
+  root against every fp16 input; ``update_centres`` against a one-hot fp32
+  matrix product.
 
 Parity unpinned: exact ``torch.topk`` tie order for unstructured K
 (compression.py:82) -- this oracle fixes "lowest index wins" as the CUDA
-encoders do; fp16 distance ties of the reference V k-means (it rounds
-distances to fp16) -- this oracle uses exact distances.
+encoders do.  The reference's fp32 accumulation order inside its GEMMs and
+reductions is unknown; where an exact sum lies within fp32 rounding of an fp16
+midpoint either rounding is possible, and ``value_ambiguous`` names those
+tokens instead of choosing.
 """
 
 import numpy as np
@@ -358,6 +373,9 @@ def linspace_indices(t, count):
 def assign(data, centers):
     """Exact (float64) nearest centre with the lowest index on ties; also the margin.
 
+    This is the K rule: ``cdist`` of fp32 data (compression.py:27, 38-39) whose
+    mm formulation accumulates in fp32, so the reference's ids equal the exact
+    ones wherever the margin exceeds fp32 rounding.
     Returns (ids [N], margin [N]) where margin = second-best minus best squared
     distance -- a small margin marks an assignment that fp32 rounding may flip.
     """
@@ -370,45 +388,186 @@ def assign(data, centers):
     return ids, margin
 
 
-def kmeans(x, count, iterations, *, value=False):
-    """Lloyd k-means per (batch, head), float64 (compression.py:19-53).
+def _half_norm_exact(a):
+    """Exact sum of the fp16-rounded squares of fp16 rows (float64; a*a is exact there)."""
+    a = np.asarray(a, dtype=np.float16).astype(np.float64)
+    return (a * a).astype(np.float16).astype(np.float64).sum(-1)
 
-    x: fp16 [B, H, T, 128].  K (value=False) keeps an empty cluster's previous
-    centre; V (value=True) zeroes it, rounds every updated centre to fp16 and
-    uses count = min(count, T).
+
+def half_norms(a):
+    """``a.pow(2).sum(-1)`` of fp16 rows as torch evaluates it: each square
+    rounded to fp16, the sum accumulated in fp32 and rounded to fp16.  This
+    restatement sums exactly and rounds once (the accumulation order only
+    matters within fp32 rounding of a rounding midpoint)."""
+    return _half_norm_exact(a).astype(np.float16)
+
+
+def _fp16_sqrt(d16):
+    """Correctly rounded fp16 square root of clamped fp16 values (torch's
+    ``clamp_min_(0).sqrt_()`` on half; float64 sqrt then one rounding is exact
+    here since 53 >= 2*11 + 2)."""
+    return np.sqrt(np.maximum(np.asarray(d16, dtype=np.float64), 0.0)).astype(np.float16)
+
+
+def value_distances(x, centers):
+    """fp16 distances of ``torch.cdist(x, c, compute_mode="use_mm_for_euclid_dist")``
+    on fp16 data (compression.py:27, 38).
+
+    The mm formulation is one fp16 GEMM of [-2x, |x|^2, 1] against
+    [c, 1, |c|^2]: the norms are fp16 (``half_norms``), the 130-term dot
+    product accumulates in fp32 and is rounded to fp16, then clamped at zero
+    and square-rooted in fp16.  This restatement forms the 130-term sum exactly
+    and rounds it once.  Returns (s16 fp16 [..., N, C], exact pre-rounding
+    squared distance float64 [..., N, C]).
+    """
+    x = np.asarray(x, dtype=np.float16)
+    c = np.asarray(centers, dtype=np.float16)
+    xn = half_norms(x).astype(np.float64)
+    cn = half_norms(c).astype(np.float64)
+    dot = x.astype(np.float64) @ np.swapaxes(c.astype(np.float64), -1, -2)
+    d = xn[..., :, None] + cn[..., None, :] - 2.0 * dot
+    return _fp16_sqrt(d.astype(np.float16)), d
+
+
+def assign_value(x, centers):
+    """V assignment: argmin over the fp16 distances, lowest index on ties
+    (``argmin`` returns the first minimum)."""
+    s16, _ = value_distances(x, centers)
+    return np.argmin(s16.astype(np.float32), axis=-1)
+
+
+def _midpoint_distance(v, rel):
+    """True where an exact value v lies within rel * |v| of an fp16 rounding
+    midpoint (so an fp32 accumulation of it may round to either neighbour)."""
+    v = np.asarray(v, dtype=np.float64)
+    h = v.astype(np.float16)
+    up = np.nextafter(h, np.float16(np.inf)).astype(np.float64)
+    dn = np.nextafter(h, np.float16(-np.inf)).astype(np.float64)
+    hv = h.astype(np.float64)
+    mids = np.stack(((hv + up) / 2, (hv + dn) / 2))
+    return (np.abs(mids - v) <= rel * np.abs(v) + 1e-30).any(0)
+
+
+def value_ambiguous(x, centers, rel=2.0 ** -20):
+    """Tokens whose V id could differ from ``assign_value`` when the fp32
+    accumulations of the reference (or of any other implementation) round
+    differently from the exact sums: a 130-term distance or a norm within
+    ``rel`` of an fp16 rounding midpoint.  A distance is taken as the interval
+    of its two possible fp16 roundings; the token is unambiguous when the
+    oracle's winner stays the lowest-indexed minimum over every choice."""
+    x = np.asarray(x, dtype=np.float16)
+    c = np.asarray(centers, dtype=np.float16)
+    s16, d = value_distances(x, c)
+    xs, cs = _half_norm_exact(x), _half_norm_exact(c)
+    xamb = _midpoint_distance(xs, rel)                         # [..., N]
+    camb = _midpoint_distance(cs, rel)                         # [..., C]
+    scale = np.abs(x.astype(np.float64)) @ np.swapaxes(np.abs(c.astype(np.float64)), -1, -2)
+    width = rel * (xs[..., :, None] + cs[..., None, :] + 2.0 * scale)
+    # a norm near a midpoint moves every distance of its row or column by up to one fp16 ulp
+    ulp = lambda v: np.abs(np.nextafter(v.astype(np.float16), np.float16(np.inf)).astype(np.float64)
+                           - v.astype(np.float16).astype(np.float64))
+    width = width + np.where(xamb, ulp(xs), 0.0)[..., :, None] + np.where(camb, ulp(cs), 0.0)[..., None, :]
+    lo = _fp16_sqrt((d - width).astype(np.float16)).astype(np.float64)
+    hi = _fp16_sqrt((d + width).astype(np.float16)).astype(np.float64)
+    w = np.argmin(s16.astype(np.float32), axis=-1)
+    hw = np.take_along_axis(hi, w[..., None], axis=-1)
+    idx = np.arange(c.shape[-2])
+    before = idx < w[..., None]
+    beats = np.where(before, lo <= hw, lo < hw)              # another centre that could win or tie first
+    beats &= idx != w[..., None]
+    return beats.any(-1)
+
+
+def incremental_value_distances(x, centers):
+    """V distances of the decode-group assignment (compression.py:61-64):
+    fp32(fp16(|x|^2 + |c|^2) - 2 * fp32(x . c)), the norms in fp16 (the
+    inputs' dtype), their sum rounded to fp16, the product fp32.  Restated with
+    an exact dot product, so ids agree with the reference's away from fp32 ties.
+    Returns float64 [..., N, C]."""
+    x = np.asarray(x, dtype=np.float16)
+    c = np.asarray(centers, dtype=np.float16)
+    e = (half_norms(x).astype(np.float64)[..., :, None] + half_norms(c).astype(np.float64)[..., None, :])
+    e = e.astype(np.float16).astype(np.float64)
+    dot = x.astype(np.float64) @ np.swapaxes(c.astype(np.float64), -1, -2)
+    return e - 2.0 * dot
+
+
+def update_centres(data, ids, previous, count, *, value=False):
+    """One Lloyd update from given ids (compression.py:40-52).
+
+    Member sums are exact (float64; the reference's fp32 GEMM sums equal them
+    within fp32 rounding), counted in fp32, divided in fp32.  K keeps an empty
+    cluster's previous centre and stays fp32; V rounds each quotient to fp16
+    (``.to(data.dtype)``) and an empty cluster becomes 0 / 1 = 0.
+    data float [BH, T, 128], ids int [BH, T], previous [BH, C, 128].
+    """
+    data = np.asarray(data, dtype=np.float64)
+    onehot = np.eye(count)[np.asarray(ids)]                  # [BH, T, C]
+    counts = onehot.sum(1)[..., None]
+    sums = (np.swapaxes(onehot, 1, 2) @ data).astype(np.float32)
+    mean = (sums / np.maximum(counts, 1).astype(np.float32)).astype(np.float32)
+    if value:
+        return f16(mean).astype(np.float64)
+    return np.where(counts > 0, mean.astype(np.float64), np.asarray(previous, dtype=np.float64))
+
+
+def kmeans(x, count, iterations, *, value=False):
+    """Lloyd k-means per (batch, head) (compression.py:19-53).
+
+    x: fp16 [B, H, T, 128].  K (value=False) assigns by exact distances (the
+    fp32 rule, ``assign``), keeps an empty cluster's previous centre and
+    carries fp32 centres; V (value=True) assigns by the fp16 ``cdist`` rule
+    (``assign_value``), zeroes an empty cluster, rounds every updated centre to
+    fp16 and uses count = min(count, T).
     Returns (centers fp16 [B,H,C,128], ids int32 [B,H,T], min_margin float) where
     ids come from the last assignment (made against the pre-update centres)
-    and centres from the last update.  Requires T >= count (the reference's
-    random-init branch for T < count is not deterministic).
+    and centres from the last update.  min_margin is the smallest
+    second-minus-best distance (squared for K, fp16 distance for V).  Requires
+    T >= count (the reference's random-init branch for T < count is not
+    deterministic).
     """
     b, h, t, _ = x.shape
     if value:
         count = min(count, t)
     if t < count:
         raise ValueError("oracle k-means needs T >= count")
-    data = np.asarray(x, dtype=np.float16).astype(np.float64).reshape(b * h, t, D)
+    x16 = np.asarray(x, dtype=np.float16).reshape(b * h, t, D)
+    data = x16.astype(np.float64)
     idx = linspace_indices(t, count)
     centers = data[:, idx].copy()
     ids = None
     min_margin = np.inf
     for _ in range(iterations):
-        ids, margin = assign(data, centers)
+        if value:
+            s16, _ = value_distances(x16, centers.astype(np.float16))
+            s = np.sort(s16.astype(np.float64), axis=-1)
+            ids = np.argmin(s16.astype(np.float32), axis=-1)
+            margin = s[..., 1] - s[..., 0] if count > 1 else np.full(ids.shape, np.inf)
+        else:
+            ids, margin = assign(data, centers)
         min_margin = min(min_margin, float(margin.min()))
-        onehot = np.eye(count)[ids]                          # [BH, T, C]
-        counts = onehot.sum(1)[..., None]
-        sums = np.swapaxes(onehot, 1, 2) @ data
-        mean = sums / np.maximum(counts, 1)
-        # V centres are stored back in fp16 after every update (compression.py:48-50)
-        centers = f16(mean).astype(np.float64) if value else np.where(counts > 0, mean, centers)
+        centers = update_centres(data, ids, centers, count, value=value)
     return f16(centers.reshape(b, h, count, D)), ids.reshape(b, h, t).astype(np.int32), min_margin
 
 
 def incremental_cluster(x, centers, max_clusters, *, value=False):
-    """Append the group mean while under the cap, then assign (compression.py:56-69)."""
+    """Append the group mean while under the cap, then assign (compression.py:56-69).
+
+    The appended centre is ``x.mean(2)`` in fp16 (fp32 accumulation, one
+    rounding).  K assigns by exact distances (``cdist`` of fp32 data); V by
+    ``incremental_value_distances``, lowest index on ties.  Returns (centres
+    fp16, ids int32, margin) with margin the smallest second-minus-best distance.
+    """
     x = np.asarray(x, dtype=np.float16)
     c = np.asarray(centers, dtype=np.float16)
     if c.shape[2] < max_clusters:
-        mean = f16(x.astype(np.float32).mean(2, keepdims=True))
+        mean = (x.astype(np.float64).sum(2, keepdims=True) / x.shape[2]).astype(np.float16)
         c = np.concatenate((c, mean), axis=2)
-    ids, margin = assign(x.astype(np.float64), c.astype(np.float64))
+    if value:
+        d = incremental_value_distances(x, c)
+        ids = np.argmin(d, axis=-1)
+        srt = np.sort(d, axis=-1)
+        margin = srt[..., 1] - srt[..., 0] if d.shape[-1] > 1 else np.full(ids.shape, np.inf)
+    else:
+        ids, margin = assign(x.astype(np.float64), c.astype(np.float64))
     return c, ids.astype(np.int32), float(margin.min())

@@ -74,18 +74,22 @@ def _workspace(nbytes, device):
     return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
 
 
-# RoPE tables keyed by their frequencies: (device, data_ptr, version) of a
-# caller's inv_freq tensor, or (device, "theta", base).  Compressed tokens keep
-# their positions, so one table serves every layer and decode step.
+# RoPE tables, one per frequency set: the caller's inv_freq tensor (keyed by
+# its storage address and version, the tensor itself held so that the address
+# cannot be reused) or the theta-derived set (keyed by theta).  Compressed
+# tokens keep their positions, so one table serves every layer and decode
+# step.  Tables are never freed: a table that grows is replaced, and the
+# replaced one stays alive in _RETIRED, because a captured HIP graph or work
+# still queued on another stream may hold its address.  Growth is geometric
+# (powers of two), so the retired tables add at most the size of the live one.
+# For graph capture: make one eager call at the largest position first, so
+# that no table is allocated while capturing.
 _ROPE_TABLES = {}
-_ROPE_TABLE_LIMIT = 16
+_RETIRED = []
 
 
 def _rope_table(freq, key, positions, source=None):
-    """fp32 [P, 128] table covering positions [0, positions), P a power of two.
-
-    ``source`` is the tensor whose address is part of ``key``; the cache keeps
-    it alive so that the address cannot be reused by other frequencies."""
+    """fp32 [P, 128] table covering positions [0, positions), P a power of two."""
     entry = _ROPE_TABLES.get(key)
     if entry is not None and entry[0].shape[0] >= positions:
         return entry[0]
@@ -94,20 +98,31 @@ def _rope_table(freq, key, positions, source=None):
     with torch.cuda.device(freq.device):
         _lib.check(_lib.lib().reskv_rope_table(freq.data_ptr(), count, table.data_ptr(), _stream(freq.device)),
                    "rope_table")
-    if len(_ROPE_TABLES) >= _ROPE_TABLE_LIMIT:
-        _ROPE_TABLES.pop(next(iter(_ROPE_TABLES)))
+    if entry is not None:
+        _RETIRED.append(entry)
     _ROPE_TABLES[key] = (table, source)
     return table
 
 
 def _rope(inv_freq, rope_base, dev, positions):
-    """(frequencies, table) for the caller's inv_freq [64] or the theta-derived set."""
-    freq = _frequencies(inv_freq, rope_base, dev)
+    """(fp32 frequencies, table) for the caller's inv_freq [64] (any float
+    dtype; the key is the caller's tensor, not a converted copy) or the
+    theta-derived set."""
     if inv_freq is not None and inv_freq.numel():
-        key, source = (dev, inv_freq.data_ptr(), inv_freq._version), inv_freq
-    else:
-        key, source = (dev, "theta", float(rope_base)), None
-    return freq, _rope_table(freq, key, positions, source)
+        _require(inv_freq.numel() == 64 and inv_freq.is_floating_point(), "inv_freq must be fp32 [64]")
+        key = (dev, inv_freq.untyped_storage().data_ptr(), inv_freq.storage_offset(), inv_freq._version)
+        entry = _ROPE_TABLES.get(key)
+        if entry is not None and entry[0].shape[0] >= positions:
+            return entry[1][1], entry[0]
+        freq = _frequencies(inv_freq.float(), rope_base, dev)
+        table = _rope_table(freq, key, positions, (inv_freq, freq))
+        return freq, table
+    key = (dev, "theta", float(rope_base))
+    entry = _ROPE_TABLES.get(key)
+    if entry is not None and entry[0].shape[0] >= positions:
+        return entry[1], entry[0]
+    freq = _frequencies(None, rope_base, dev)
+    return freq, _rope_table(freq, key, positions, freq)
 
 
 def _frequencies(inv_freq, rope_base, device):
@@ -241,10 +256,16 @@ def kmeans_kv(k, v, init_k, init_v, iterations):
     return (outs[0], ids[0]), (outs[1], ids[1])
 
 
-def kmeans_assign(x, centers):
-    """Nearest-centre ids, lowest index on ties. x fp16 [BH,T,128]; centres fp32 [BH,C,128]."""
+def kmeans_assign(x, centers, value=False):
+    """Nearest-centre ids, lowest index on ties. x fp16 [BH,T,128]; centres fp32 [BH,C,128].
+
+    value=False: fp32 distances (K); value=True: the decode-group V rule,
+    fp32(fp16(|x|^2 + |c|^2) - 2 x.c) with fp16 norms.
+    """
     _require(x.dtype == torch.float16 and x.dim() == 3 and x.shape[2] == 128, "x must be fp16 [BH,T,128]")
-    _require(centers.dtype == torch.float32 and centers.dim() == 3, "centres must be fp32 [BH,C,128]")
+    _require(centers.dtype == torch.float32 and centers.dim() == 3 and centers.shape[2] == 128,
+             "centres must be fp32 [BH,C,128]")
+    _require(centers.shape[0] == x.shape[0], "x and centres must have the same leading dimension")
     dev = _dev_check(x, centers)
     bh, t, _ = x.shape
     c = centers.shape[1]
@@ -252,7 +273,7 @@ def kmeans_assign(x, centers):
     L = _lib.lib()
     ws = _workspace(L.reskv_kmeans_workspace_bytes(bh, t, c), dev)
     with torch.cuda.device(dev):
-        _lib.check(L.reskv_kmeans_assign(x.data_ptr(), centers.data_ptr(), ids.data_ptr(), bh, t, c,
+        _lib.check(L.reskv_kmeans_assign(x.data_ptr(), centers.data_ptr(), ids.data_ptr(), bh, t, c, int(bool(value)),
                                          ws.data_ptr(), ws.numel(), _stream(dev)), "kmeans_assign")
     return ids
 
@@ -390,6 +411,57 @@ class StepDecoder:
         return dst.view(self.b, self.nh, 1, 128)
 
 
+def decode_step(query2d, cache, num_q_heads, *, position, start_position, scaling, inv_freq, rope_theta,
+                splits=0, recent=None):
+    """One decode call over a CompressedKV: fp16 [B*Hq, 128].
+
+    query2d fp16 [B*Hq, 128] pre-RoPE, contiguous.  ``recent`` is None or
+    (rotated query fp16 [B*Hq, 128], rotated K and V fp16 [B, Hk, Tr, 128],
+    contiguous); the split merge then joins the window before it writes the
+    output (``reskv_decode_recent``), so a step is two kernel launches.
+    """
+    kdesc, vdesc, keep = cache_descriptors(cache)
+    dev = query2d.device
+    _dev_check(query2d, *keep, contiguous=False)
+    b, kh = cache.key.centroids.shape[:2]
+    nh, t = int(num_q_heads), cache.seq_len
+    freq, table = _rope(inv_freq, rope_theta, dev, int(start_position) + t)
+    L = _lib.lib()
+    out = _empty((b * nh, 128), torch.float16, dev)
+    ws = _workspace(L.reskv_decode_workspace_bytes(b, nh, kh, t, int(splits)), dev)
+    common = (query2d.data_ptr(), kdesc, vdesc, freq.data_ptr(), table.data_ptr(), b, nh, kh, t,
+              int(start_position), int(position), float(scaling), int(splits))
+    with torch.cuda.device(dev):
+        if recent is None:
+            _lib.check(L.reskv_decode_rope(*common, out.data_ptr(), None, None, ws.data_ptr(), ws.numel(),
+                                           _stream(dev)), "decode")
+        else:
+            q_rot, k_rec, v_rec = recent
+            _dev_check(q_rot, k_rec, v_rec)
+            tr = int(k_rec.shape[2])
+            _lib.check(L.reskv_decode_recent(*common, q_rot.data_ptr(), k_rec.data_ptr(), v_rec.data_ptr(), tr, tr,
+                                             out.data_ptr(), ws.data_ptr(), ws.numel(), _stream(dev)), "decode")
+    return out
+
+
+def _check_recent_inputs(comp_out, comp_m, comp_l, v_recent, nh_kv, nh):
+    """Shape and dtype checks shared by both merge_recent ops
+    (reskv/csrc/attention.cu:850-868, cluster_mass.cu:1469-1476); returns (B, Tr)."""
+    _require(comp_out.dim() == 2 and comp_out.shape[1] == 128, "comp_out must be [B*nh, 128]")
+    _require(comp_out.dtype == torch.float16, "comp_out must be fp16")
+    _require(comp_m.dim() == 1 and comp_l.dim() == 1, "comp_m/comp_l must be [B*nh]")
+    _require(comp_m.dtype == torch.float32 and comp_l.dtype == torch.float32, "comp_m/comp_l must be fp32")
+    _require(nh_kv > 0 and nh % nh_kv == 0, "num_q_heads must be divisible by num_kv_heads")
+    _require(nh // nh_kv in (1, 2, 4, 8), f"Unsupported GQA ratio: {nh // max(nh_kv, 1)}")
+    _require(comp_out.shape[0] % nh == 0, "Q/comp_out batch-head mismatch")
+    b = comp_out.shape[0] // nh
+    _require(comp_m.shape[0] == b * nh and comp_l.shape[0] == b * nh, "comp_m/comp_l must be [B*nh]")
+    _require(v_recent.dim() == 4 and v_recent.shape[3] == 128, "v_recent must be [B, nh_kv, T, 128]")
+    _require(v_recent.dtype == torch.float16, "v_recent must be fp16")
+    _require(v_recent.shape[0] == b and v_recent.shape[1] == nh_kv, "v_recent shape mismatch")
+    return b, int(v_recent.shape[2])
+
+
 def _make_cluster_mass():
     def decode_fp16(Q, kc, ki, kp, kbitmap, vc, vi, vp, vbitmap, nh_kv, nh, start_pos, pos_q, rope_base,
                     scaling, return_stats, splits, inv_freq):
@@ -432,14 +504,11 @@ def _make_cluster_mass():
 
     def merge_recent(comp_out, comp_m, comp_l, scores_recent, v_recent, nh_kv, nh):
         """Joint softmax with precomputed fp32 recent scores (reskv/csrc/cluster_mass.cu:1461-1508)."""
-        _require(comp_out.dim() == 2 and comp_out.shape[1] == 128, "comp_out must be [B*nh, 128]")
         nh_kv, nh = int(nh_kv), int(nh)
-        _require(nh % nh_kv == 0, "num_q_heads must be divisible by num_kv_heads")
+        b, tr = _check_recent_inputs(comp_out, comp_m, comp_l, v_recent, nh_kv, nh)
         _require(scores_recent.dtype == torch.float32 and scores_recent.dim() == 3, "scores must be fp32 [B,nh,Tr]")
-        _require(v_recent.dtype == torch.float16 and v_recent.dim() == 4, "v_recent must be fp16 [B,nh_kv,Tr,128]")
+        _require(tuple(scores_recent.shape) == (b, nh, tr), "scores_recent must be [B, nh, T_recent]")
         dev = _dev_check(comp_out, comp_m, comp_l, scores_recent, v_recent)
-        b = comp_out.shape[0] // nh
-        tr = scores_recent.shape[2]
         out = torch.empty_like(comp_out)
         with torch.cuda.device(dev):
             _lib.check(_lib.lib().reskv_merge_recent_scores(
@@ -486,13 +555,16 @@ def _make_attention(plan):
 
     def merge_recent(comp_out, comp_m, comp_l, Q_rope, k_recent, v_recent, nh_kv, nh, scaling):
         """Joint softmax with dense rotated recent tokens (reskv/csrc/attention.cu:839-906)."""
-        _require(comp_out.dim() == 2 and comp_out.shape[1] == 128, "comp_out must be [B*nh, 128]")
         nh_kv, nh = int(nh_kv), int(nh)
-        _require(nh % nh_kv == 0, "num_q_heads must be divisible by num_kv_heads")
-        _require(k_recent.dim() == 4 and k_recent.shape == v_recent.shape, "recent K/V must be [B,nh_kv,Tr,128]")
+        b, tr = _check_recent_inputs(comp_out, comp_m, comp_l, v_recent, nh_kv, nh)
+        _require(Q_rope.dim() == 2 and Q_rope.shape[1] == 128, "Q_rope must be [B*nh, 128]")
+        _require(Q_rope.dtype == torch.float16, "Q_rope must be fp16")
+        _require(Q_rope.shape[0] == comp_out.shape[0], "Q/comp_out batch-head mismatch")
+        _require(k_recent.dim() == 4 and k_recent.shape[3] == 128, "k_recent must be [B, nh_kv, T, 128]")
+        _require(k_recent.dtype == torch.float16, "k_recent must be fp16")
+        _require(k_recent.shape == v_recent.shape, "v_recent shape mismatch")
+        _require(tr > 0, "T_recent must be > 0")
         dev = _dev_check(comp_out, comp_m, comp_l, Q_rope, k_recent, v_recent)
-        b = comp_out.shape[0] // nh
-        tr = k_recent.shape[2]
         out = torch.empty_like(comp_out)
         with torch.cuda.device(dev):
             _lib.check(_lib.lib().reskv_merge_recent_qk(

@@ -44,7 +44,7 @@ SIGNATURES = {
     "reskv_compress_structured_int4": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
     "reskv_kmeans_workspace_bytes": (_i64, [_i, _i, _i]),
     "reskv_kmeans": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp, _i64, _vp]),
-    "reskv_kmeans_assign": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp, _i64, _vp]),
+    "reskv_kmeans_assign": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _vp, _i64, _vp]),
     "reskv_kmeans_kv": (_i, [_vp] * 8 + [_i, _i, _i, _i, _vp, _i64, _vp]),
     "reskv_decode_workspace_bytes": (_i64, [_i, _i, _i, _i, _i]),
     "reskv_decode_splits": (_i, [_i, _i, _i, _i, _i]),

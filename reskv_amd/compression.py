@@ -79,7 +79,8 @@ def _incremental_cluster(x, centers, config, *, value=False):
     if centers.shape[2] < config.max_clusters:
         centers = torch.cat((centers, x.mean(2, keepdim=True)), dim=2)
     ext = load_extension("compression", device_index=x.device.index or 0)
-    ids = ext.kmeans_assign(x.reshape(b * h, t, d).contiguous(), centers.reshape(b * h, -1, d).float().contiguous())
+    ids = ext.kmeans_assign(x.reshape(b * h, t, d).contiguous(), centers.reshape(b * h, -1, d).float().contiguous(),
+                            value)
     return centers, ids.reshape(b, h, t)
 
 

@@ -16,10 +16,17 @@
 // Assignment (kmeans_assign_kernel): the distance GEMM S^T = C X^T runs on the
 // matrix cores (v_mfma_f32_16x16x32f16).  Tokens are fp16 already and
 // C X^T = C_hi X^T + C_lo X^T keeps fp32 accuracy (c_hi * x and c_lo * x are
-// exact in fp32, sums are fp32).  d(x, c) = |c|^2 - 2 <x, c> (|x|^2 is common
-// to a token); each lane holds one token's distances to 4 centres per 16, so
-// the argmin (lowest index on ties) is a scan in registers and two lane swaps
-// across the four lanes sharing the token.  Member sums are a second matrix-core
+// exact in fp32, sums are fp32).  Each lane holds one token's distances to 4
+// centres per 16, so the argmin (lowest index on ties) is a scan in registers
+// and two lane swaps across the four lanes sharing the token.  The distance
+// follows the rule the reference applies to the tensor:
+//   K (compression.py:38, fp32 cdist): |c|^2 - 2 <x, c> in fp32 (|x|^2 is
+//     common to a token);
+//   V, Lloyd (compression.py:27, 38, fp16 cdist in the mm formulation):
+//     fp16(|x|^2_h + |c|^2_h - 2 <x, c>), clamped at zero, square-rooted to
+//     fp16; |.|^2_h is the fp16 sum of fp16-rounded squares;
+//   V, decode groups (compression.py:61-64):
+//     fp16(|x|^2_h + |c|^2_h) - 2 <x, c> in fp32.  Member sums are a second matrix-core
 // product, onehot(ids)^T X, whose X operand comes from the wave's 16-token tile
 // through LDS transpose reads; the member counts are the same product against
 // an all-ones operand.  One-hot entries and tokens are exact in fp16 and the
@@ -78,21 +85,25 @@ __device__ __forceinline__ int operand_slot_half(int c, int d) {
 
 // Centre c of one problem's tables from the fp32 centre v held by threads
 // 0..127 (channel = thread).  Every thread of the workgroup calls it (it holds
-// a barrier); threads >= 128 pass active = false.
-__device__ __forceinline__ void store_tables(float v, bool active, bool pad, int split_lo, int c,
+// a barrier); threads >= 128 pass active = false.  K rows carry an fp16 lo
+// part and the fp32 |c|^2; V rows (fp16 centres) carry the fp16 norm of the
+// reference's cdist, the fp16 sum of fp16-rounded squares.
+__device__ __forceinline__ void store_tables(float v, bool active, bool pad, bool value, int c,
                                              uint16_t* __restrict__ hi, uint16_t* __restrict__ lo,
                                              float* __restrict__ norm, float* s_w) {
+#pragma clang fp contract(off)
     const int t = threadIdx.x;
     if (active) {
         const uint16_t hb = f2h(v);
         const int o = operand_slot_half(c, t);
         hi[o] = hb;
-        lo[o] = split_lo ? f2h(v - h2f(hb)) : (uint16_t)0;
-        const float w = wave_sum(v * v);
+        lo[o] = value ? (uint16_t)0 : f2h(v - h2f(hb));
+        const float sq = value ? h2f(f2h(v * v)) : v * v;  // V: v is fp16, v*v exact in fp32
+        const float w = wave_sum(sq);
         if ((t & 63) == 0) s_w[t >> 6] = w;
     }
     __syncthreads();
-    if (t == 0) *norm = pad ? INFINITY : s_w[0] + s_w[1];
+    if (t == 0) *norm = pad ? INFINITY : (value ? h2f(f2h(s_w[0] + s_w[1])) : s_w[0] + s_w[1]);
 }
 
 // Where the problems live: problems [0, split) are rows of tensor 0 and
@@ -103,6 +114,7 @@ struct Problems {
     int32_t* ids[2];       // ids int32 [problems, T]
     uint16_t* out[2];      // final centres fp16 [problems, C, 128]
     int split, vfrom;
+    int vgroup;            // V problems assign by the decode-group rule instead of Lloyd's
 };
 __device__ __forceinline__ int side_of(const Problems& P, long bh) { return bh >= P.split ? 1 : 0; }
 
@@ -116,7 +128,82 @@ __global__ void __launch_bounds__(kDim) kmeans_prep_kernel(const float* __restri
     const bool pad = c >= C;
     const float v = pad ? 0.0f : centers[(bh * C + c) * kDim + threadIdx.x];
     const long head = bh * Cp * kDim;
-    store_tables(v, true, pad, bh < vfrom, c, thi + head, tlo + head, tnorm + bh * Cp + c, s_w);
+    store_tables(v, true, pad, bh >= vfrom, c, thi + head, tlo + head, tnorm + bh * Cp + c, s_w);
+}
+
+// |c|^2 of centre r of a lane's four
+__device__ __forceinline__ float cnorm(float4 n, int r) { return r == 0 ? n.x : r == 1 ? n.y : r == 2 ? n.z : n.w; }
+
+// (distance, index) minimum over the four lanes holding one token (lanes
+// col + 16 g): every lane ends with the token's nearest centre.
+__device__ __forceinline__ void token_argmin(float& bd, int& bi) {
+    const auto pd = __builtin_amdgcn_permlane32_swap((uint32_t)f2i(bd), (uint32_t)f2i(bd), false, false);
+    const auto pi = __builtin_amdgcn_permlane32_swap((uint32_t)bi, (uint32_t)bi, false, false);
+    bd = i2f((int)pd[0]);
+    bi = (int)pi[0];
+    argmin_step(bd, bi, i2f((int)pd[1]), (int)pi[1]);
+    const auto qd = __builtin_amdgcn_permlane16_swap((uint32_t)f2i(bd), (uint32_t)f2i(bd), false, false);
+    const auto qi = __builtin_amdgcn_permlane16_swap((uint32_t)bi, (uint32_t)bi, false, false);
+    bd = i2f((int)qd[0]);
+    bi = (int)qi[0];
+    argmin_step(bd, bi, i2f((int)qd[1]), (int)qi[1]);
+}
+__device__ __forceinline__ float token_min(float v) {
+    const auto a = __builtin_amdgcn_permlane32_swap((uint32_t)f2i(v), (uint32_t)f2i(v), false, false);
+    v = fminf(i2f((int)a[0]), i2f((int)a[1]));
+    const auto b = __builtin_amdgcn_permlane16_swap((uint32_t)f2i(v), (uint32_t)f2i(v), false, false);
+    return fminf(i2f((int)b[0]), i2f((int)b[1]));
+}
+__device__ __forceinline__ int token_min_index(int v) {
+    const auto a = __builtin_amdgcn_permlane32_swap((uint32_t)v, (uint32_t)v, false, false);
+    v = min((int)a[0], (int)a[1]);
+    const auto b = __builtin_amdgcn_permlane16_swap((uint32_t)v, (uint32_t)v, false, false);
+    return min((int)b[0], (int)b[1]);
+}
+
+// fp16 norm of a token as the reference's fp16 cdist forms it: each square
+// rounded to fp16, summed in fp32 (this lane's 32 channels, then the four lanes
+// of the token; the pairwise sums are commutative, so all four lanes agree),
+// rounded to fp16.
+__device__ __forceinline__ float token_half_norm(const uint4* xq) {
+#pragma clang fp contract(off)
+    float acc = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const uint32_t w[4] = {xq[q].x, xq[q].y, xq[q].z, xq[q].w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float a = h2f((uint16_t)(w[j] & 0xFFFFu)), b = h2f((uint16_t)(w[j] >> 16));
+            acc += h2f(f2h(a * a));  // a * a is exact in fp32; one rounding to fp16
+            acc += h2f(f2h(b * b));
+        }
+    }
+    const auto p = __builtin_amdgcn_permlane32_swap((uint32_t)f2i(acc), (uint32_t)f2i(acc), false, false);
+    acc = i2f((int)p[0]) + i2f((int)p[1]);
+    const auto q = __builtin_amdgcn_permlane16_swap((uint32_t)f2i(acc), (uint32_t)f2i(acc), false, false);
+    acc = i2f((int)q[0]) + i2f((int)q[1]);
+    return h2f(f2h(acc));
+}
+
+// For a non-negative fp16 value d (as float): M^2, with M the midpoint between
+// the correctly rounded fp16 square root of d and the next fp16 value above
+// it.  An fp16 value e has the same fp16 root as d exactly when d <= e < M^2
+// (a root is never exactly a midpoint; M has 12 significant bits, so M^2 is
+// exact in fp32).  The hardware root is within one fp16 step after rounding
+// and is corrected against the midpoints on both sides.
+__device__ __forceinline__ float root_bound_sq(float d) {
+#pragma clang fp contract(off)
+    const uint16_t sb = f2h(__builtin_sqrtf(d));
+    float sv = h2f(sb);
+    const float up = h2f((uint16_t)(sb + 1)), dn = sb ? h2f((uint16_t)(sb - 1)) : 0.0f;
+    const float mhi = 0.5f * (sv + up), mlo = 0.5f * (sv + dn);
+    uint16_t rb = sb;
+    if (mhi * mhi < d) rb = (uint16_t)(sb + 1);
+    else if (sb && mlo * mlo > d) rb = (uint16_t)(sb - 1);
+    if (rb >= 0x7C00u) return INFINITY;  // root is infinite: only d itself qualifies
+    sv = h2f(rb);
+    const float m = 0.5f * (sv + h2f((uint16_t)(rb + 1)));
+    return m * m;
 }
 
 // One workgroup: tokens [chunk * kChunk, +kChunk) of problem bh; wave w takes
@@ -145,6 +232,8 @@ __global__ void __launch_bounds__(kThreads) kmeans_assign_kernel(
     const long pb = bh - (side ? P.split : 0);
     const uint16_t* __restrict__ x = P.x[side] + pb * T * kDim;
     int32_t* __restrict__ ids = P.ids[side] + pb * T;
+    const bool vrule = bh >= P.vfrom;  // workgroup-uniform
+    const bool vgroup = P.vgroup != 0;
 
     // token operand: lane (col, grp) holds token t0 + col, channels 32 q + 8 grp +
     // [0, 8) for piece q, so the four lanes of a token read 64 contiguous bytes;
@@ -226,33 +315,67 @@ __global__ void __launch_bounds__(kThreads) kmeans_assign_kernel(
                     acc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_h8(b_lo(nb, q)), as_h8(xr[s][q]), acc[nb], 0, 0, 0);
             }
         }
-        // nearest of this lane's centres, scanned in increasing index order (a
-        // strict < keeps the lower index on ties), then across the four row
-        // groups holding the same token
-        float bd = fmaf(-2.0f, acc[0][0], cn[0].x);
-        int bi = 4 * grp;
+        int bi;
+        if (!vrule) {
+            // K: nearest of this lane's centres, scanned in increasing index
+            // order (a strict < keeps the lower index on ties), then across the
+            // four row groups holding the same token
+            float bd = fmaf(-2.0f, acc[0][0], cn[0].x);
+            bi = 4 * grp;
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
+            for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                if (nb == 0 && r == 0) continue;
-                const float nr = r == 0 ? cn[nb].x : r == 1 ? cn[nb].y : r == 2 ? cn[nb].z : cn[nb].w;
-                const float d = fmaf(-2.0f, acc[nb][r], nr);
-                const bool take = d < bd;
-                bd = take ? d : bd;
-                bi = take ? nb * 16 + 4 * grp + r : bi;
+                for (int r = 0; r < 4; ++r) {
+                    if (nb == 0 && r == 0) continue;
+                    const float d = fmaf(-2.0f, acc[nb][r], cnorm(cn[nb], r));
+                    const bool take = d < bd;
+                    bd = take ? d : bd;
+                    bi = take ? nb * 16 + 4 * grp + r : bi;
+                }
+            token_argmin(bd, bi);
+        } else {
+            const float xn = token_half_norm(xr[s]);
+            if (vgroup) {
+                // decode groups: fp32(fp16(|x|^2 + |c|^2) - 2 <x, c>), lowest index on ties
+                float bd = INFINITY;
+                bi = 1 << 20;
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const float e = h2f(f2h(xn + cnorm(cn[nb], r)));
+                        const float d = fmaf(-2.0f, acc[nb][r], e);
+                        const bool take = d < bd;
+                        bd = take ? d : bd;
+                        bi = take ? nb * 16 + 4 * grp + r : bi;
+                    }
+                token_argmin(bd, bi);
+            } else {
+                // Lloyd: fp16 cdist.  The winner is the lowest index whose fp16
+                // root equals the smallest one: with dmin the smallest fp16
+                // squared distance and M the midpoint above its fp16 root,
+                // that is every d < M^2 (M^2 is exact in fp32), or d == dmin
+                // when the root is infinite.
+                float d16[NB][4];
+                float dmin = INFINITY;
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const float d = fmaf(-2.0f, acc[nb][r], xn + cnorm(cn[nb], r));
+                        d16[nb][r] = fmaxf(h2f(f2h(d)), 0.0f);
+                        dmin = fminf(dmin, d16[nb][r]);
+                    }
+                dmin = token_min(dmin);
+                const float thr = root_bound_sq(dmin);
+                bi = 1 << 20;
+#pragma unroll
+                for (int nb = NB - 1; nb >= 0; --nb)
+#pragma unroll
+                    for (int r = 3; r >= 0; --r)
+                        if (d16[nb][r] < thr || d16[nb][r] == dmin) bi = nb * 16 + 4 * grp + r;
+                bi = token_min_index(bi);
             }
-        {
-            const auto pd = __builtin_amdgcn_permlane32_swap((uint32_t)f2i(bd), (uint32_t)f2i(bd), false, false);
-            const auto pi = __builtin_amdgcn_permlane32_swap((uint32_t)bi, (uint32_t)bi, false, false);
-            bd = i2f((int)pd[0]);
-            bi = (int)pi[0];
-            argmin_step(bd, bi, i2f((int)pd[1]), (int)pi[1]);
-            const auto qd = __builtin_amdgcn_permlane16_swap((uint32_t)f2i(bd), (uint32_t)f2i(bd), false, false);
-            const auto qi = __builtin_amdgcn_permlane16_swap((uint32_t)bi, (uint32_t)bi, false, false);
-            bd = i2f((int)qd[0]);
-            bi = (int)qi[0];
-            argmin_step(bd, bi, i2f((int)qd[1]), (int)qi[1]);
         }
         // every lane of column col now holds the id of token t0 + col
         if (grp == 0 && t0 + col < T) ids[t0 + col] = bi;
@@ -377,7 +500,7 @@ __global__ void __launch_bounds__(kParts * kDim) kmeans_update_kernel(
     }
     if (thi == nullptr) return;  // uniform over the workgroup
     const long head = bh * Cp * kDim;
-    store_tables(nv, par == 0, false, !value_mode, c, thi + head, tlo + head, tnorm + bh * Cp + c, s_w);
+    store_tables(nv, par == 0, false, value_mode, c, thi + head, tlo + head, tnorm + bh * Cp + c, s_w);
 }
 
 // Workspace: fp32 centres, the fp16 hi/lo tables and norms, chunk partials;
@@ -496,18 +619,20 @@ extern "C" int64_t reskv_kmeans_workspace_bytes(int BH, int T, int C) {
 }
 
 extern "C" int reskv_kmeans_assign(const void* x, const float* centers, int32_t* ids, int BH, int T, int C,
-                                   void* workspace, int64_t workspace_bytes, void* stream) {
+                                   int value_mode, void* workspace, int64_t workspace_bytes, void* stream) {
     RESKV_REQUIRE(x && centers && ids, "null pointer argument");
     RESKV_REQUIRE(BH > 0 && T > 0, "problem sizes must be positive");
     RESKV_REQUIRE(C >= 1 && C <= kMaxClusters, "centroid count must be in [1, 64]");
+    RESKV_REQUIRE(value_mode == 0 || value_mode == 1, "value_mode must be 0 (K) or 1 (V)");
     RESKV_REQUIRE(workspace && workspace_bytes >= reskv_kmeans_workspace_bytes(BH, T, C),
                   "k-means workspace too small");
     if (check_pointers(x, workspace)) return 1;
     const Layout L = layout(BH, T, C);
     const Tables tb = tables_of(workspace, L);
-    const Problems P{{(const uint16_t*)x, (const uint16_t*)x}, {ids, ids}, {nullptr, nullptr}, BH, BH};
+    const int vfrom = value_mode ? 0 : BH;
+    const Problems P{{(const uint16_t*)x, (const uint16_t*)x}, {ids, ids}, {nullptr, nullptr}, BH, vfrom, 1};
     hipStream_t st = (hipStream_t)stream;
-    if (launch_prep(centers, tb, BH, C, L.Cp, BH, st)) return 1;
+    if (launch_prep(centers, tb, BH, C, L.Cp, vfrom, st)) return 1;
     return launch_assign(P, tb, nullptr, nullptr, BH, T, C, L, st);
 }
 
@@ -523,7 +648,7 @@ extern "C" int reskv_kmeans(const void* x, const float* centers_init, void* cent
     if (check_pointers(x, workspace)) return 1;
     const uint16_t* xh = (const uint16_t*)x;
     uint16_t* out = (uint16_t*)centers_out;
-    const Problems P{{xh, xh}, {ids, ids}, {out, out}, BH, value_mode ? 0 : BH};
+    const Problems P{{xh, xh}, {ids, ids}, {out, out}, BH, value_mode ? 0 : BH, 0};
     const float* const init[2] = {centers_init, centers_init};
     return run_kmeans(P, init, BH, T, C, iterations, workspace, (hipStream_t)stream);
 }
@@ -539,7 +664,7 @@ extern "C" int reskv_kmeans_kv(const void* k, const void* v, const float* init_k
                   "k-means workspace too small");
     if (check_pointers(k, workspace) || check_pointers(v, workspace)) return 1;
     const Problems P{{(const uint16_t*)k, (const uint16_t*)v}, {ids_k, ids_v}, {(uint16_t*)out_k, (uint16_t*)out_v},
-                     BH, BH};
+                     BH, BH, 0};
     const float* const init[2] = {init_k, init_v};
     return run_kmeans(P, init, 2 * BH, T, C, iterations, workspace, (hipStream_t)stream);
 }

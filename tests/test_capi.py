@@ -32,7 +32,7 @@ def test_library_exports_every_declared_symbol():
     for name in declared_functions():
         assert hasattr(lib, name), name
         assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
-    assert lib.reskv_abi_version() == 2
+    assert lib.reskv_abi_version() == 3
 
 
 def _err(status):
@@ -106,3 +106,93 @@ def test_split_and_workspace_sizing():
     assert lib.reskv_decode_splits(1, 32, 8, 5, 20) == 5  # explicit split counts are capped at T
     assert lib.reskv_decode_splits(1, 32, 8, 8192, 20) == 20
     assert lib.reskv_kmeans_workspace_bytes(16, 8192, 32) > 0
+
+
+# ---------------------------------------------------------------------------
+# merge_recent input checks run before any launch (CPU tensors never reach
+# the library: a shape or dtype error is raised first, then the device check)
+# ---------------------------------------------------------------------------
+
+def _recent_args(b=2, nh=8, kh=2, tr=5, width=128, m_dtype=None, heads=None):
+    import torch
+
+    comp = torch.zeros(b * nh, 128, dtype=torch.float16)
+    m = torch.zeros(b * nh, dtype=m_dtype or torch.float32)
+    l = torch.zeros(b * nh, dtype=torch.float32)
+    v = torch.zeros(b, heads or kh, tr, width, dtype=torch.float16)
+    return comp, m, l, v
+
+
+@pytest.mark.parametrize("bad,match", [
+    ({"width": 64}, "v_recent must be"),
+    ({"heads": 3}, "v_recent shape mismatch"),
+    ({"m_dtype": "f16"}, "comp_m/comp_l must be fp32"),
+])
+def test_deferred_merge_recent_rejects_bad_shapes(bad, match):
+    import torch
+    from reskv_amd._extension import load_extension
+
+    if bad.get("m_dtype") == "f16":
+        bad = dict(bad, m_dtype=torch.float16)
+    comp, m, l, v = _recent_args(**bad)
+    scores = torch.zeros(2, 8, v.shape[2], dtype=torch.float32)
+    ext = load_extension("cluster_mass")
+    with pytest.raises(RuntimeError, match=match):
+        ext.merge_recent(comp, m, l, scores, v, 2, 8)
+
+
+def test_deferred_merge_recent_rejects_score_shape():
+    import torch
+    from reskv_amd._extension import load_extension
+
+    comp, m, l, v = _recent_args()
+    ext = load_extension("cluster_mass")
+    with pytest.raises(RuntimeError, match="scores_recent must be"):
+        ext.merge_recent(comp, m, l, torch.zeros(2, 8, 4, dtype=torch.float32), v, 2, 8)
+    with pytest.raises(RuntimeError, match="Unsupported GQA ratio"):
+        ext.merge_recent(comp, m, l, torch.zeros(2, 8, 5, dtype=torch.float32), v, 3, 9)
+
+
+@pytest.mark.parametrize("bad,match", [
+    ({"width": 64}, "v_recent must be"),
+    ({"heads": 4}, "v_recent shape mismatch"),
+    ({"tr": 0}, "T_recent must be > 0"),
+])
+def test_per_token_merge_recent_rejects_bad_shapes(bad, match):
+    import torch
+    from reskv_amd._extension import load_extension
+
+    comp, m, l, v = _recent_args(**bad)
+    k = torch.zeros(v.shape, dtype=torch.float16)
+    if bad.get("heads"):
+        k = torch.zeros(2, 2, v.shape[2], 128, dtype=torch.float16)
+    q = torch.zeros(16, 128, dtype=torch.float16)
+    ext = load_extension("attention")
+    with pytest.raises(RuntimeError, match=match):
+        ext.merge_recent(comp, m, l, q, k, v, 2, 8, 0.1)
+
+
+def test_per_token_merge_recent_rejects_short_key_rows():
+    import torch
+    from reskv_amd._extension import load_extension
+
+    comp, m, l, v = _recent_args()
+    ext = load_extension("attention")
+    with pytest.raises(RuntimeError, match="k_recent must be"):
+        ext.merge_recent(comp, m, l, torch.zeros(16, 128, dtype=torch.float16),
+                         torch.zeros(2, 2, 5, 64, dtype=torch.float16), v, 2, 8, 0.1)
+    with pytest.raises(RuntimeError, match="all tensors must be on the same GPU"):
+        ext.merge_recent(comp, m, l, torch.zeros(16, 128, dtype=torch.float16),
+                         torch.zeros(2, 2, 5, 128, dtype=torch.float16), v, 2, 8, 0.1)
+
+
+def test_attention_rejects_recent_rows_that_are_not_128_wide():
+    import torch
+    from reskv_amd._attention import _recent_window
+
+    q = torch.zeros(1, 8, 1, 128, dtype=torch.float16)
+    bad = (q, torch.zeros(1, 2, 4, 64, dtype=torch.float16), torch.zeros(1, 2, 4, 64, dtype=torch.float16))
+    with pytest.raises(ValueError, match="recent Q/K/V shapes"):
+        _recent_window(bad, q, 1, 2)
+    empty = (q, torch.zeros(1, 2, 0, 128, dtype=torch.float16), torch.zeros(1, 2, 0, 128, dtype=torch.float16))
+    assert _recent_window(empty, q, 1, 2) is None

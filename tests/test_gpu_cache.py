@@ -146,3 +146,28 @@ def test_step_decoder_one_merge_launch_equals_two(device, sparsity, ring_len):
     assert torch.equal(out, ref)
     again = step.run(q, pos, qr, ring_k, ring_v, ring_len, stride)
     assert torch.equal(again, ref)
+
+
+def test_attend_with_a_ring_of_several_chunks(device):
+    """recent_size 256 + group 64: the ring holds up to 320 tokens, read in place
+    by the split merge's multi-chunk join; checked against the oracle."""
+    cfg = ResKVKernelConfig(sparsity=0.5, num_clusters=8, max_clusters=12, group_size=64, recent_size=256)
+    k, v = _inputs(700, device, seed=41, b=1, h=2)
+    g = seeded(42)
+    freq = (500000.0 ** (-torch.arange(64).float() / 64)).to(device)
+    layer = ResKVLayerCache(cfg)
+    layer.update(k[:, :, :400], v[:, :, :400], {"raw_keys": k[:, :, :400]})
+    checked = 0
+    for t in range(400, 700):
+        layer.update(k[:, :, t:t + 1], v[:, :, t:t + 1], {"raw_keys": k[:, :, t:t + 1]})
+        if layer.live <= 128 or t % 23:
+            continue
+        q = torch.randn(1, 8, 1, 128, generator=g).half().to(device)
+        pos = layer.length - 1
+        qr = torch.from_numpy(o.rotate(np_(q).astype(np.float64), np.array([pos]), np_(freq))).half().to(device)
+        got = layer.attend(q, qr, scaling=128 ** -0.5, inv_freq=freq)
+        ring = (qr, layer.keys[:, :, :layer.live], layer.values[:, :, :layer.live])
+        ref = expected_attention(q, layer.compressed, position=pos, inv_freq=freq, recent=ring)
+        assert float(np.abs(np_(got).astype(np.float64) - ref).max()) <= ATOL, t
+        checked += 1
+    assert checked >= 3

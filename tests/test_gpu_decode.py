@@ -279,3 +279,57 @@ def test_query_position_before_cache_rejected(device):
     cache = compress(k, v, clustering=c)
     with pytest.raises(ValueError, match="precedes"):
         attention(q, cache, position=10)
+
+
+@pytest.mark.parametrize("sparsity,layout", [(0.5, "unstructured"), (0.75, "structured")])
+def test_deferred_merge_recent_with_fp32_scores(device, sparsity, layout):
+    """The deferred family's merge_recent(comp_out, m, l, scores, v_recent)
+    (cluster_mass.cu:1461-1508) fed as reskv/_attention.py:135-143 feeds it:
+    fp32 scores q_rot . k_rot * scale, against the oracle's joint softmax."""
+    from reskv_amd._extension import load_extension
+
+    k, v, q = outlier_kv(2, 2, 640, seed=33)
+    cfg = ResKVKernelConfig(sparsity=sparsity, layout=layout, centroid_fusion="deferred", num_clusters=16)
+    cache = compress(k, v, cfg)
+    ext = load_extension("cluster_mass", cache.key.plan)
+    freq = theta_freq()
+    pos, tr, scale = 700, 57, 128 ** -0.5
+    g = torch.Generator().manual_seed(34)
+    kr = (torch.randn(2, 2, tr, 128, generator=g) * 2).half().to(device)
+    vr = torch.randn(2, 2, tr, 128, generator=g).half().to(device)
+    qr = torch.from_numpy(o.rotate(np_(q).astype(np.float64), np.array([pos]), np_(freq))).half().to(device)
+    qf = q.reshape(-1, 128).contiguous()
+    kc, ki, kp, km, _ = cache.key._native
+    vc, vi, vp, vm, _ = cache.value._native
+    args = (2, 8, 0, pos, 500000.0, scale, True, 0, freq)
+    if layout == "unstructured":
+        out, m, l = ext.decode_fp16(qf, kc, ki, kp, km, vc, vi, vp, vm, *args)
+    else:
+        e = qf.new_empty(0)
+        out, m, l = ext.decode_structured_fp16(qf, kc, ki, kp, km, e, vc, vi, vp, vm, e, *args)
+    scores = torch.matmul(qr.float().reshape(2, 2, 4, 128), kr.float().transpose(-1, -2)) * scale
+    merged = ext.merge_recent(out, m, l, scores.reshape(2, 8, tr).contiguous(), vr, 2, 8)
+    ref = expected_attention(q, cache, position=pos, inv_freq=freq, recent=(qr, kr, vr))
+    assert _max_err(merged.reshape(2, 8, 1, 128), ref) <= ATOL
+    # the same joint softmax as the in-kernel-score path
+    fused = attention(q, cache, position=pos, inv_freq=freq, recent=(qr, kr, vr))
+    assert _max_err(merged.reshape(2, 8, 1, 128), np_(fused).astype(np.float64)) <= 1e-3
+
+
+@pytest.mark.parametrize("tr", [129, 300])
+def test_recent_window_longer_than_one_chunk(device, tr):
+    """Recent windows above 128 tokens take the merge's multi-chunk online
+    rescale (the model reaches them with recent_size >= 128)."""
+    k, v, q = outlier_kv(2, 2, 512, seed=35)
+    cache = compress(k, v, ResKVKernelConfig(sparsity=0.5, num_clusters=16))
+    freq = theta_freq()
+    pos = 512 + tr
+    g = torch.Generator().manual_seed(36)
+    kr = (torch.randn(2, 2, tr, 128, generator=g) * 2).half().to(device)
+    vr = torch.randn(2, 2, tr, 128, generator=g).half().to(device)
+    # a late token with a large score moves the running maximum in the last chunk
+    kr[:, :, tr - 3] = 8.0
+    qr = torch.from_numpy(o.rotate(np_(q).astype(np.float64), np.array([pos]), np_(freq))).half().to(device)
+    out = attention(q, cache, position=pos, inv_freq=freq, recent=(qr, kr, vr))
+    ref = expected_attention(q, cache, position=pos, inv_freq=freq, recent=(qr, kr, vr))
+    assert _max_err(out, ref) <= ATOL

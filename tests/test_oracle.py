@@ -160,6 +160,41 @@ def test_multibit_codes_and_dequantisation(bits):
     assert cent.shape == x.shape
 
 
+def test_multibit_known_answer_uses_the_fp16_scale():
+    """Hand-computed INT4 codes (compression.cu:339-360).
+
+    amax = 1.0, so the scale is fp16(1/7) = 0.142822265625 (10-bit mantissa
+    146).  Channel 5 holds r = 1.5 * 0.142822265625 = 0.2142333984375 (fp16,
+    mantissa 731): divided by the fp16 scale it is exactly 1.5, which rounds
+    half-to-even to 2.  Divided by the unrounded fp32 quotient 1/7 it is
+    1.4996..., which rounds to 1, so a restatement that skips the fp16
+    rounding point fails here.  The second token has amax = 0.875, so its
+    scale is exactly 0.125; channel 9 holds 0.3125, 2.5 steps, which
+    half-to-even rounds to 2 (half-away-from-zero would give 3).
+    """
+    res = np.zeros((2, 128), dtype=np.float32)
+    res[0, 0] = 1.0
+    res[0, 5] = 0.2142333984375
+    res[0, 7] = -0.2142333984375
+    res[1, 3] = 0.875                      # amax = 7 * 0.125: scale exactly 0.125
+    res[1, 9] = 0.3125                     # 2.5 steps
+    res[1, 11] = -0.3125
+    x = res.astype(np.float16)[None, None]
+    c = np.zeros((1, 1, 1, 128), dtype=np.float16)
+    ids = np.zeros((1, 1, 2), dtype=np.int64)
+    qt, sc = o.encode_multibit(x, c, ids, 64, 4)
+    assert sc[0, 0, 0] == np.float16(0.142822265625) and sc[0, 0, 1] == np.float16(0.125)
+    assert np.float16(0.142822265625).view(np.uint16) == 0x3092
+    words = qt.view(np.uint32)[0, 0]
+    nib = lambda t, d: int((words[t, d // 8] >> np.uint32(4 * (d % 8))) & np.uint32(15))
+    assert nib(0, 0) == 7 and nib(0, 5) == 2 and nib(0, 7) == (-2 & 15)
+    assert nib(1, 3) == 7 and nib(1, 9) == 2 and nib(1, 11) == (-2 & 15)
+    # every other channel is 0 (kept zeros and dropped channels alike)
+    others = [(t, d) for t in range(2) for d in range(128) if (t, d) not in
+              {(0, 0), (0, 5), (0, 7), (1, 3), (1, 9), (1, 11)}]
+    assert all(nib(t, d) == 0 for t, d in others)
+
+
 # ---------------------------------------------------------------------------
 # reconstruction round trips
 # ---------------------------------------------------------------------------
@@ -352,3 +387,110 @@ def test_incremental_cluster_appends_mean_until_cap():
     assert c2.shape[2] == 4 and np.allclose(c2[0, 0, 3], x[0, 0].astype(np.float32).mean(0), atol=1e-3)
     c3, _, _ = o.incremental_cluster(x, c2, max_clusters=4)
     assert c3.shape[2] == 4
+
+
+# ---------------------------------------------------------------------------
+# V k-means arithmetic, pinned against CPU torch's own ops
+# ---------------------------------------------------------------------------
+
+def _torch():
+    return pytest.importorskip("torch")
+
+
+def test_fp16_sqrt_is_correctly_rounded_for_every_half():
+    h = np.arange(0, 0x7C01, dtype=np.uint16).view(np.float16)  # 0 .. +inf
+    got = o._fp16_sqrt(h).astype(np.float64)
+    exact = np.sqrt(h.astype(np.float64))
+    up = np.nextafter(got.astype(np.float16), np.float16(np.inf)).astype(np.float64)
+    dn = np.nextafter(got.astype(np.float16), np.float16(0)).astype(np.float64)
+    finite = np.isfinite(exact)
+    # nearest: the exact root lies within half an ulp on both sides
+    with np.errstate(invalid="ignore"):
+        assert np.all(np.abs(exact - got)[finite] <= np.maximum(up - got, got - dn)[finite] / 2)
+    torch = _torch()
+    t = torch.from_numpy(h.copy()).clamp_min(0).sqrt()
+    assert np.array_equal(t.numpy().view(np.uint16), got.astype(np.float16).view(np.uint16))
+
+
+def test_half_norms_match_torch():
+    torch = _torch()
+    rng = np.random.default_rng(11)
+    x = (rng.standard_normal((3, 500, 128)) * rng.lognormal(0, 1, (1, 1, 128))).astype(np.float16)
+    ref = torch.from_numpy(x).pow(2).sum(-1).numpy()
+    got = o.half_norms(x)
+    amb = o._midpoint_distance(o._half_norm_exact(x), 2.0 ** -20)
+    assert np.array_equal(got[~amb], ref[~amb]) and amb.mean() < 0.01
+
+
+@pytest.mark.parametrize("scale", [1.0, 4.0])
+def test_value_distances_match_torch_cdist(scale):
+    """The restated V distance equals CPU torch's fp16 cdist (mm formulation)
+    bit for bit wherever the token is not flagged, and so do the ids; the
+    exact-distance rule does not (it differs on ~0.5% of ids)."""
+    torch = _torch()
+    rng = np.random.default_rng(12)
+    x = (rng.standard_normal((4, 2000, 128)) * scale).astype(np.float16)
+    c = x[:, o.linspace_indices(2000, 32)]
+    ref = torch.cdist(torch.from_numpy(x), torch.from_numpy(c), compute_mode="use_mm_for_euclid_dist")
+    s16, _ = o.value_distances(x, c)
+    amb = o.value_ambiguous(x, c)
+    assert amb.mean() < 0.01
+    ref_ids = ref.float().argmin(-1).numpy()
+    ids = o.assign_value(x, c)
+    assert np.array_equal(ids[~amb], ref_ids[~amb])
+    assert (s16 == ref.numpy()).mean() > 0.999
+    exact_ids, _ = o.assign(x.astype(np.float64), c.astype(np.float64))
+    assert (exact_ids != ref_ids).mean() > 0.001  # the K rule would not pin V
+
+
+def test_value_ties_take_the_lowest_index():
+    """Two different fp16 squared distances with one fp16 root: the lower
+    index wins although its squared distance is larger."""
+    x = np.zeros((1, 1, 128), dtype=np.float16)
+    c = np.zeros((1, 3, 128), dtype=np.float16)
+    c[0, 0, 1], c[0, 0, 2] = 16.0, 0.5   # |x - c|^2 = 256.25 -> sqrt 16.0078... rounds to 16
+    c[0, 1, 0] = 16.0                    # 256 -> 16
+    c[0, 2, 3] = 16.015625               # 256.5 -> 16.0156 (next fp16): farther
+    s16, d = o.value_distances(x, c)
+    assert d[0, 0, 0] == 256.25 and d[0, 0, 1] == 256.0
+    assert s16[0, 0, 0] == s16[0, 0, 1] == np.float16(16)
+    assert o.assign_value(x, c)[0, 0] == 0
+    exact_ids, _ = o.assign(x.astype(np.float64), c.astype(np.float64))
+    assert exact_ids[0, 0] == 1
+
+
+def test_incremental_value_rule_matches_torch_expression():
+    torch = _torch()
+    rng = np.random.default_rng(13)
+    x = rng.standard_normal((2, 4, 64, 128)).astype(np.float16)
+    c = rng.standard_normal((2, 4, 21, 128)).astype(np.float16)
+    tx, tc = torch.from_numpy(x), torch.from_numpy(c)
+    dist = (tx ** 2).sum(-1, keepdim=True) + (tc ** 2).sum(-1).unsqueeze(2)   # compression.py:63
+    dist = dist - 2 * torch.matmul(tx.float(), tc.float().transpose(-2, -1))   # compression.py:64
+    d = o.incremental_value_distances(x, c)
+    assert np.abs(d - dist.double().numpy()).max() <= 1e-4
+    assert np.array_equal(np.argmin(d, -1), dist.argmin(-1).numpy())
+    c2, ids, _ = o.incremental_cluster(x, c, 22, value=True)
+    assert np.array_equal(c2[:, :, 21], tx.mean(2).numpy())                       # compression.py:60
+    d2 = o.incremental_value_distances(x, c2)
+    assert np.array_equal(ids, np.argmin(d2, -1))
+
+
+@pytest.mark.parametrize("value", [False, True])
+def test_update_centres_matches_one_hot_product(value):
+    torch = _torch()
+    rng = np.random.default_rng(14)
+    x = rng.standard_normal((2, 300, 128)).astype(np.float16)
+    ids = rng.integers(0, 7, (2, 300))       # cluster 7 stays empty
+    prev = rng.standard_normal((2, 8, 128))
+    got = o.update_centres(x.astype(np.float64), ids, prev, 8, value=value)
+    tx = torch.from_numpy(x).float()
+    oh = torch.nn.functional.one_hot(torch.from_numpy(ids), 8).float()
+    counts = oh.sum(1).unsqueeze(-1)
+    sums = torch.bmm(oh.transpose(1, 2), tx)
+    if value:
+        ref = (sums / counts.clamp_min(1)).half().double().numpy()
+        assert np.abs(got - ref).max() <= 2 ** -10 and not got[:, 7].any()
+    else:
+        ref = torch.where(counts > 0, sums / counts.clamp_min(1), torch.from_numpy(prev).float()).double().numpy()
+        assert np.abs(got - ref).max() <= 1e-6 and np.array_equal(got[:, 7], prev[:, 7])
