@@ -204,6 +204,27 @@ int reskv_decode_recent(const void* q, const reskv_ctensor* k, const reskv_ctens
                         const void* k_recent, const void* v_recent, int Tr, int r_stride, void* out,
                         void* workspace, int64_t workspace_bytes, void* stream);
 
+/* Bytes of device scratch that reskv_decode_recent_noalloc holds per GPU. */
+#define RESKV_NOALLOC_SCRATCH_BYTES (8LL << 20)
+
+/* reskv_decode_recent without a workspace argument: it allocates nothing.
+ * No counterpart in the reference; it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  The split-K partial records go to a file-scope
+ * device array of RESKV_NOALLOC_SCRATCH_BYTES (8 MiB) that each GPU holds
+ * until the process ends; its address is looked up once per device
+ * (hipGetSymbolAddress) on the first call.  Sizes whose partials exceed it
+ * (reskv_decode_workspace_bytes(B, Hq, H, T, splits) > 8 MiB; the automatic
+ * split count stays below that up to B*Hq = 10,000 rows) are rejected with an
+ * error.  Every call on a GPU shares that GPU's array: calls that overlap on
+ * one GPU race.  Arguments and result are those of reskv_decode_recent
+ * (Tr = 0: plain decode). */
+int reskv_decode_recent_noalloc(const void* q, const reskv_ctensor* k, const reskv_ctensor* v,
+                                const float* inv_freq, const float* rope_table, int B, int Hq, int H, int T,
+                                int start_pos, int pos_q, float scaling, int splits, const void* q_rope,
+                                const void* k_recent, const void* v_recent, int Tr, int r_stride, void* out,
+                                void* stream);
+
 /* Dense fp16 decode attention (the uncompressed baseline at the same shapes):
  * q fp16 [B*Hq,128] pre-RoPE, k fp16 [B,H,*,128] pre-RoPE, v fp16 [B,H,*,128]:
  * the first T tokens of rows of t_stride tokens (t_stride<=0: T), so that a

@@ -54,6 +54,8 @@ SIGNATURES = {
                                _i, _i, _f, _i, _vp, _vp, _vp, _vp, _i64, _vp]),
     "reskv_decode_recent": (_i, [_vp, ctypes.POINTER(CTensor), ctypes.POINTER(CTensor), _vp, _vp, _i, _i, _i, _i,
                                  _i, _i, _f, _i, _vp, _vp, _vp, _i, _i, _vp, _vp, _i64, _vp]),
+    "reskv_decode_recent_noalloc": (_i, [_vp, ctypes.POINTER(CTensor), ctypes.POINTER(CTensor), _vp, _vp, _i, _i,
+                                         _i, _i, _i, _i, _f, _i, _vp, _vp, _vp, _i, _i, _vp, _vp]),
     "reskv_rope_table": (_i, [_vp, _i, _vp, _vp]),
     "reskv_merge_recent_scores": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _vp]),
     "reskv_merge_recent_qk": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _f, _vp, _vp]),

@@ -23,6 +23,8 @@
 
 #include <math.h>
 
+#include <mutex>
+
 using namespace reskv;
 
 namespace {
@@ -1416,6 +1418,63 @@ extern "C" int reskv_decode_recent(const void* q, const reskv_ctensor* k, const 
     const int kf = dfmt_of(k), vf = dfmt_of(v);
     return run_decode(q, kf, to_dt(k, kf, T), vf, to_dt(v, vf, T), inv_freq, rope_table, B, Hq, H, T, start_pos,
                       pos_q, scaling, splits, out, nullptr, nullptr, workspace, workspace_bytes, stream, &rc);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free decode: the split-K partial records live in one file-scope
+// device array instead of a caller workspace.  Each GPU the library runs on
+// holds its own copy until the process ends.  The partial kernel writes every
+// record the merge kernel reads, so nothing in it has to start at zero; the
+// array keeps the last call's records.  Calls that overlap on one GPU (two
+// host threads, or two streams without ordering) race on it.
+// ---------------------------------------------------------------------------
+constexpr int64_t kNoAllocScratchBytes = RESKV_NOALLOC_SCRATCH_BYTES;
+constexpr int kMaxDevices = 64;
+__device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace {
+std::once_flag g_scratch_once[kMaxDevices];
+void* g_scratch_ptr[kMaxDevices] = {};
+hipError_t g_scratch_err[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device (its name is only a host
+// stand-in).  Looked up once per device; returns null with the error message
+// set when the device or the lookup fails.
+void* scratch_on_current_device() {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        reskv_host::set_error("no current HIP device (or device index >= %d)", kMaxDevices);
+        return nullptr;
+    }
+    std::call_once(g_scratch_once[dev], [dev]() {
+        void* ptr = nullptr;
+        g_scratch_err[dev] = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        g_scratch_ptr[dev] = g_scratch_err[dev] == hipSuccess ? ptr : nullptr;
+    });
+    if (g_scratch_ptr[dev] == nullptr) {
+        reskv_host::set_error("hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                              hipGetErrorString(g_scratch_err[dev]));
+        return nullptr;
+    }
+    return g_scratch_ptr[dev];
+}
+}  // namespace
+
+extern "C" int reskv_decode_recent_noalloc(const void* q, const reskv_ctensor* k, const reskv_ctensor* v,
+                                           const float* inv_freq, const float* rope_table, int B, int Hq, int H,
+                                           int T, int start_pos, int pos_q, float scaling, int splits,
+                                           const void* q_rope, const void* k_recent, const void* v_recent, int Tr,
+                                           int r_stride, void* out, void* stream) {
+    RESKV_REQUIRE(B > 0 && Hq > 0 && H > 0 && T > 0, "batch, head and token counts must be positive");
+    const int64_t need = reskv_decode_workspace_bytes(B, Hq, H, T, splits);
+    RESKV_REQUIRE(need <= kNoAllocScratchBytes,
+                  "reskv_decode_recent_noalloc: these sizes need %lld bytes of split-K scratch; the "
+                  "allocation-free entry point holds %lld (use reskv_decode_recent with a workspace)",
+                  (long long)need, (long long)kNoAllocScratchBytes);
+    void* ws = scratch_on_current_device();
+    if (ws == nullptr) return 1;
+    return reskv_decode_recent(q, k, v, inv_freq, rope_table, B, Hq, H, T, start_pos, pos_q, scaling, splits,
+                               q_rope, k_recent, v_recent, Tr, r_stride, out, ws, kNoAllocScratchBytes, stream);
 }
 
 extern "C" int reskv_decode(const void* q, const reskv_ctensor* k, const reskv_ctensor* v,

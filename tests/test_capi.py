@@ -196,3 +196,12 @@ def test_attention_rejects_recent_rows_that_are_not_128_wide():
         _recent_window(bad, q, 1, 2)
     empty = (q, torch.zeros(1, 2, 0, 128, dtype=torch.float16), torch.zeros(1, 2, 0, 128, dtype=torch.float16))
     assert _recent_window(empty, q, 1, 2) is None
+
+
+def test_noalloc_decode_rejects_sizes_beyond_its_scratch_before_any_device_call():
+    L = _lib.lib()
+    # 64 x 8 rows x 256 splits of 776-byte partial records: far above the 8 MiB array
+    status = L.reskv_decode_recent_noalloc(None, None, None, None, None, 64, 8, 2, 256, 0, 300, 0.1, 256,
+                                           None, None, None, 0, 0, None, None)
+    assert status != 0 and "allocation-free" in L.reskv_last_error().decode()
+    assert L.reskv_decode_workspace_bytes(32, 32, 8, 8192, 0) <= 8 << 20
