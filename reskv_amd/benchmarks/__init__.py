@@ -1,3 +1,3 @@
-"""Benchmark harness (counterpart of the reference's ``benchmarks`` package):
-``kernels`` (API sweep), ``inference`` (one checkpoint, ResKV or dense),
-``compare`` (sequential runs plus report validation) and the shared ``timing``."""
+"""Benchmark commands: ``kernels`` (API sweep), ``inference`` (one local
+checkpoint, ResKV or dense), ``compare`` (sequential runs and report
+validation); ``timing`` (the timed greedy decode) and ``common`` are shared."""

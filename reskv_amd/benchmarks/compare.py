@@ -1,7 +1,7 @@
-"""Run ResKV and dense inference benchmarks in separate sequential processes and
-check that their reports are comparable (benchmarks/compare.py of the reference;
-the Mustafar baseline is not part of this build).  Run as
-``python -m reskv_amd.benchmarks.compare``."""
+"""Run ResKV and dense inference for each batch size in separate, sequential
+processes, check that the reports are comparable, and write a summary.
+``python -m reskv_amd.benchmarks.compare --model <dir> ...`` (the reference's
+benchmarks/compare.py without its Mustafar method, which is out of scope)."""
 
 import argparse
 import json
@@ -10,90 +10,98 @@ import subprocess
 import sys
 from pathlib import Path
 
-from .._io import write_json
-from .timing import add_arguments, add_model_arguments, validate_arguments, validate_gpu
+from .common import check_run, declare_run, require_gpu, save_json
 
-_SAME = ("model", "model_dtype", "batch_size", "input_length", "new_tokens", "seed", "input_ids_sha256",
-         "git_commit", "source_sha256", "gpu", "torch", "hip", "repeats", "warmup")
+# report fields that must agree across the methods of one batch size
+SHARED_FIELDS = ("model", "model_dtype", "batch_size", "input_length", "new_tokens", "seed", "input_ids_sha256",
+                 "git_commit", "source_sha256", "gpu", "torch", "hip", "repeats", "warmup")
+SUMMARY_FIELDS = ("prefill_ms", "decode_ms", "tpot_ms", "throughput_tps")
 
 
 def validate_reports(reports):
-    """Reject comparisons whose runs differ in inputs, environment or decode counts."""
-    first = reports[0]
-    for report in reports:
-        for field in _SAME:
-            if report[field] != first[field]:
-                raise ValueError(f"comparison mismatch in {field}")
-        if len(report["records"]) != report["repeats"]:
+    """Raise ValueError unless the reports describe the same inputs and environment,
+    hold ``repeats`` records each, and every record decoded new_tokens - 1 steps with
+    finite final logits."""
+    base = reports[0]
+    for rep in reports:
+        mismatched = [f for f in SHARED_FIELDS if rep[f] != base[f]]
+        if mismatched:
+            raise ValueError(f"comparison mismatch in {mismatched[0]}")
+        if len(rep["records"]) != rep["repeats"]:
             raise ValueError("unexpected record count")
-        for record in report["records"]:
-            if record["decode_steps"] != report["new_tokens"] - 1 or not record["finite_last_logits"]:
-                raise ValueError("decode step count does not match output length, or nonfinite logits")
+        if any(r["decode_steps"] != rep["new_tokens"] - 1 or not r["finite_last_logits"] for r in rep["records"]):
+            raise ValueError("decode step count does not match output length, or nonfinite logits")
 
 
-def summarize(report, path):
-    records = report["records"]
+def summary_row(report, path):
+    """Median of each timing over the report's records, and the peak allocation."""
     row = {"method": report["method"], "batch_size": report["batch_size"], "result": str(path)}
-    for name in ("prefill_ms", "decode_ms", "tpot_ms", "throughput_tps"):
-        values = [record[name] for record in records if record[name] is not None]
-        row[name] = statistics.median(values) if values else None
-    row["peak_allocated_bytes"] = max(record["peak_allocated_bytes"] for record in records)
+    for name in SUMMARY_FIELDS:
+        seen = [r[name] for r in report["records"] if r[name] is not None]
+        row[name] = statistics.median(seen) if seen else None
+    row["peak_allocated_bytes"] = max(r["peak_allocated_bytes"] for r in report["records"])
     return row
 
 
-def command_for(args, method, batch_size, output):
-    command = [sys.executable, "-m", "reskv_amd.benchmarks.inference", "--method", method, "--dtype", args.dtype,
-               "--model", args.model, "--batch-size", str(batch_size), "--input-length", str(args.input_length),
-               "--new-tokens", str(args.new_tokens), "--seed", str(args.seed), "--warmup", str(args.warmup),
-               "--repeats", str(args.repeats), "--output", str(output)]
+def child_command(args, method, batch_size, output):
+    cmd = [sys.executable, "-m", "reskv_amd.benchmarks.inference", "--method", method, "--dtype", args.dtype,
+           "--model", args.model, "--batch-size", str(batch_size), "--input-length", str(args.input_length),
+           "--new-tokens", str(args.new_tokens), "--seed", str(args.seed), "--warmup", str(args.warmup),
+           "--repeats", str(args.repeats), "--output", str(output)]
     if method == "reskv":
-        command += ["--sparsity", str(args.sparsity), "--reskv-implementation", args.reskv_implementation]
-    return command
+        cmd += ["--sparsity", str(args.sparsity), "--reskv-implementation", args.reskv_implementation]
+    return cmd
+
+
+def _run_one(args, method, batch_size):
+    target = args.output / f"{method}-b{batch_size}.json"
+    log = target.with_suffix(".log")
+    target.unlink(missing_ok=True)
+    print(f"Running {method}, batch={batch_size}; log: {log}", flush=True)
+    with log.open("w", encoding="utf-8") as stream:
+        subprocess.run(child_command(args, method, batch_size, target), check=True, stdout=stream,
+                       stderr=subprocess.STDOUT)
+    report = json.loads(target.read_text(encoding="utf-8"))
+    if report["method"] != method:
+        raise ValueError("result method does not match requested method")
+    return report, target, log
 
 
 def main():
     parser = argparse.ArgumentParser(description=__doc__)
-    add_arguments(parser, batch_sizes=True)
+    declare_run(parser, many_batches=True)
     parser.add_argument("--methods", nargs="+", choices=["reskv", "dense"], default=["reskv", "dense"])
-    add_model_arguments(parser)
     parser.add_argument("--output", type=Path, default=Path("results/comparison"))
     args = parser.parse_args()
-    validate_arguments(parser, args)
+    check_run(parser, args)
     if args.dtype != "fp16" and "reskv" in args.methods:
         parser.error("comparisons including ResKV require --dtype fp16")
     if len(set(args.methods)) != len(args.methods) or len(set(args.batch_sizes)) != len(args.batch_sizes):
         parser.error("methods and batch sizes must not contain duplicates")
-    validate_gpu(parser)
+    require_gpu(parser)
     args.output.mkdir(parents=True, exist_ok=True)
     summary = {"runs": [], "errors": []}
     for batch_size in args.batch_sizes:
         reports, rows = [], []
         for method in args.methods:
-            target = args.output / f"{method}-b{batch_size}.json"
-            log = target.with_suffix(".log")
-            target.unlink(missing_ok=True)
-            print(f"Running {method}, batch={batch_size}; log: {log}", flush=True)
             try:
-                with log.open("w", encoding="utf-8") as stream:
-                    subprocess.run(command_for(args, method, batch_size, target), check=True, stdout=stream,
-                                   stderr=subprocess.STDOUT)
-                report = json.loads(target.read_text(encoding="utf-8"))
-                if report["method"] != method:
-                    raise ValueError("result method does not match requested method")
+                report, target, _ = _run_one(args, method, batch_size)
                 reports.append(report)
-                rows.append(summarize(report, target))
+                rows.append(summary_row(report, target))
             except (OSError, subprocess.CalledProcessError, ValueError, KeyError) as exc:
+                log = args.output / f"{method}-b{batch_size}.log"
                 summary["errors"].append({"method": method, "batch_size": batch_size, "error": str(exc),
                                           "log": str(log)})
-        if reports:
-            try:
-                validate_reports(reports)
-                summary["runs"].extend(rows)
-            except (ValueError, KeyError) as exc:
-                summary["errors"].append({"batch_size": batch_size, "error": str(exc)})
-    summary_path = args.output / "summary.json"
-    write_json(summary_path, summary)
-    print(f"Results: {summary_path}")
+        if not reports:
+            continue
+        try:
+            validate_reports(reports)
+            summary["runs"].extend(rows)
+        except (ValueError, KeyError) as exc:
+            summary["errors"].append({"batch_size": batch_size, "error": str(exc)})
+    path = args.output / "summary.json"
+    save_json(path, summary)
+    print(f"Results: {path}")
     if summary["errors"]:
         raise SystemExit(1)
 

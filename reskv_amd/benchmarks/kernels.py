@@ -1,39 +1,69 @@
-"""Event-timed sweep of the compression and attention APIs (benchmarks/kernels.py of the reference).
+"""Event-timed sweep of the ``compress`` and ``attention`` APIs over batch
+sizes and sparsities at one context length (the reference's
+benchmarks/kernels.py command line and record fields).  ``python -m
+reskv_amd.benchmarks.kernels [--batch-sizes 1 16] [--seq-len 8192] ...``
 
-Run as ``python -m reskv_amd.benchmarks.kernels``.  Every case is checked
-against the float32 reconstruction (``reskv_amd.reference``) before it is timed.
+Inputs follow the reference's recipe (seed 42: K, V = 0.5 N(0,1), centres
+0.1 N(0,1), random ids, one 0.5 N(0,1) query per head, 8 KV and 32 query
+heads), compressed with that external clustering so the timing excludes
+K-means.  Each record carries two checks: ``split_invariance_max_abs``, the
+largest difference between the automatic split count and 16 splits (the
+split-K merge must not change the result), and, when the caller passes a
+``checker`` (the test suite passes a float32 reconstruction), the
+``max_abs_error`` against it.
 """
 
 import argparse
 import json
-from datetime import datetime, timezone
 from pathlib import Path
 
 import torch
 
-from .. import ResKVKernelConfig
-from .._io import write_json
-from ..compression import compress
-from .._attention import attention
-from ..reference import reference_attention
-from .timing import validate_gpu
+from .. import ResKVKernelConfig, attention, compress
+from .common import median_event_ms, provenance, require_gpu, save_json
+
+KV_HEADS, QUERY_HEADS, CENTRES = 8, 32, 32
 
 
-def event_ms(fn, warmup=5, repeats=50):
-    """Median of five event-timed means of ``repeats`` back-to-back calls, in ms."""
-    for _ in range(warmup):
-        fn()
-    torch.cuda.synchronize()
-    values = []
-    for _ in range(5):
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        start.record()
-        for _ in range(repeats):
-            fn()
-        end.record()
-        end.synchronize()
-        values.append(start.elapsed_time(end) / repeats)
-    return sorted(values)[2]
+def _inputs(batch, seq_len):
+    torch.manual_seed(42)
+    shape = (batch, KV_HEADS, seq_len, 128)
+    dev = "cuda"
+    kv = [torch.randn(shape, device=dev, dtype=torch.float16) * 0.5 for _ in range(2)]
+    centres = [torch.randn(batch, KV_HEADS, CENTRES, 128, device=dev, dtype=torch.float16) * 0.1 for _ in range(2)]
+    ids = [torch.randint(CENTRES, shape[:3], device=dev, dtype=torch.int32) for _ in range(2)]
+    q = torch.randn(batch, QUERY_HEADS, 1, 128, device=dev, dtype=torch.float16) * 0.5
+    return kv, ((centres[0], ids[0]), (centres[1], ids[1])), q
+
+
+def sweep(batch_sizes, seq_len, sparsities, implementation="default", checker=None):
+    """Yield one record per (batch size, sparsity)."""
+    layout = "unstructured" if implementation == "unstructure" else "auto"
+    for batch in batch_sizes:
+        for sparsity in sparsities:
+            cfg = ResKVKernelConfig(sparsity=sparsity, layout=layout)
+            (k, v), clustering, q = _inputs(batch, seq_len)
+            make = lambda: compress(k, v, cfg, clustering=clustering)  # noqa: E731
+            cache = make()
+            decode = lambda: attention(q, cache, position=seq_len)  # noqa: E731
+            out = decode().float()
+            other = attention(q, cache, position=seq_len, splits=16).float()
+            record = {
+                "kernel_config": cfg.to_dict(),
+                "kernel_plan": cache.key.plan.to_dict(),
+                "batch_size": batch,
+                "seq_len": seq_len,
+                "decode_ms": median_event_ms(decode),
+                "compression_ms": median_event_ms(make),
+                "split_invariance_max_abs": (out - other).abs().max().item(),
+                "max_abs_error": None,
+                "cache_bytes": cache.nbytes,
+            }
+            if checker is not None:
+                record["max_abs_error"] = (out - checker(q, cache, position=seq_len).float()).abs().max().item()
+            yield record
+            del k, v, clustering, q, cache, out, other
+            torch.cuda.empty_cache()
 
 
 def main():
@@ -47,54 +77,14 @@ def main():
     args = parser.parse_args()
     if args.seq_len < 1 or min(args.batch_sizes) < 1:
         parser.error("sequence length and batch sizes must be positive")
-    validate_gpu(parser)
+    require_gpu(parser)
     records = []
-    for b in args.batch_sizes:
-        for sparsity in args.sparsities:
-            cfg = ResKVKernelConfig(sparsity=sparsity,
-                                    layout="unstructured" if args.reskv_implementation == "unstructure" else "auto")
-            torch.manual_seed(42)
-            shape = (b, 8, args.seq_len, 128)
-            k = torch.randn(shape, device="cuda", dtype=torch.float16) * 0.5
-            v = torch.randn_like(k) * 0.5
-            kc = torch.randn(b, 8, 32, 128, device="cuda", dtype=torch.float16) * 0.1
-            vc = torch.randn_like(kc) * 0.1
-            ki = torch.randint(32, shape[:3], device="cuda", dtype=torch.int32)
-            vi = torch.randint(32, shape[:3], device="cuda", dtype=torch.int32)
-            q = torch.randn(b, 32, 1, 128, device="cuda", dtype=torch.float16) * 0.5
-
-            def make(k=k, v=v, cfg=cfg, kc=kc, ki=ki, vc=vc, vi=vi):
-                return compress(k, v, cfg, clustering=((kc, ki), (vc, vi)))
-
-            cache = make()
-
-            def fn(q=q, cache=cache):
-                return attention(q, cache, position=args.seq_len)
-
-            out = fn()
-            ref = reference_attention(q, cache, position=args.seq_len)
-            torch.testing.assert_close(out.float(), ref, atol=3e-3, rtol=3e-2)
-            record = {
-                "kernel_config": cfg.to_dict(),
-                "kernel_plan": cache.key.plan.to_dict(),
-                "batch_size": b,
-                "seq_len": args.seq_len,
-                "decode_ms": event_ms(fn),
-                "compression_ms": event_ms(make),
-                "max_abs_error": (out.float() - ref).abs().max().item(),
-                "cache_bytes": cache.nbytes,
-            }
-            records.append(record)
-            print(json.dumps(record), flush=True)
-            del make, fn, k, v, q, kc, vc, ki, vi, cache, out, ref
-    write_json(args.output, {
-        "timestamp": datetime.now(timezone.utc).isoformat(),
-        "gpu": torch.cuda.get_device_name(),
-        "gpu_arch": str(getattr(torch.cuda.get_device_properties(0), "gcnArchName", "")),
-        "torch": torch.__version__,
-        "hip": torch.version.hip,
-        "records": records,
-    })
+    for rec in sweep(args.batch_sizes, args.seq_len, args.sparsities, args.reskv_implementation):
+        if rec["split_invariance_max_abs"] > 2e-3:
+            raise RuntimeError(f"split-count invariance violated: {rec}")
+        print(json.dumps(rec), flush=True)
+        records.append(rec)
+    save_json(args.output, {**provenance(), "records": records})
 
 
 if __name__ == "__main__":

@@ -1,9 +1,15 @@
-"""Compressed K/V cache containers.
+"""Compressed K/V cache containers (the ``reskv.tensors`` surface,
+reskv/tensors.py:11-162).
 
-Interface mirror of ``reskv/tensors.py:11-162``: the same fields, shape/dtype
-contract per layout, int8 cluster ids and the flattened ``_native`` views that
-the decode kernels receive.  The containers only hold device tensors; all
-arithmetic happens in the HIP library.
+A ``CompressedTensor`` is a record of device tensors whose expected dtypes and
+widths follow from its ``KernelPlan``: ``_Layout`` derives them once, and
+``_violations`` walks an ordered list of rules, raising the first one that
+fails (the order and wording are the reference's, which callers match on).
+The record also carries ``_native``: the [B*H, ...] views the C ABI receives.
+A view into a larger capacity buffer (rows of each (batch, head) block evenly
+strided, 16-byte aligned) is passed as is, so the device cache's history is
+read in place; anything else is made contiguous.  All arithmetic runs in the
+HIP library.
 """
 
 from dataclasses import dataclass, field
@@ -13,25 +19,61 @@ import torch
 from .config import KernelPlan
 
 _ID_DTYPES = (torch.int8, torch.int16, torch.int32, torch.int64)
+_STORED = ("cluster_ids", "payload", "metadata", "scale")  # tensors that grow along T
 
 
-def _rows(t: torch.Tensor) -> torch.Tensor:
-    """t when its innermost dimensions are dense (a [BH, T(, W)] block view), else a contiguous copy."""
-    inner_dense = t.stride(-1) == 1 and (t.dim() == 2 or t.stride(-2) == t.shape[-1] or t.shape[-2] == 1)
+@dataclass(frozen=True)
+class _Layout:
+    """What a plan's residual format stores per token."""
+
+    payload_dtype: torch.dtype
+    payload_width: int
+    meta: tuple | None      # (words, dtype) or None
+    scaled: bool
+
+    @staticmethod
+    def of(plan: KernelPlan) -> "_Layout":
+        spec = plan.metadata_spec
+        meta = None if spec is None else (spec[0], getattr(torch, spec[1]))
+        dtype = torch.float16 if plan.bits == 16 else torch.int32
+        return _Layout(dtype, plan.payload_width, meta, plan.bits != 16)
+
+
+def _violations(ct: "CompressedTensor"):
+    """(failed, message) pairs in the order they are checked."""
+    c, ids, p = ct.centroids, ct.cluster_ids, ct.payload
+    lay = _Layout.of(ct.plan)
+    yield c.ndim != 4 or c.shape[-1] != 128, "centroids must have shape [B,H,C,128]"
+    yield ids.ndim != 3 or ids.shape[:2] != c.shape[:2], "cluster IDs must have shape [B,H,T]"
+    yield not 1 <= c.shape[2] <= 64, "centroid count must be between 1 and 64"
+    yield p.ndim != 4 or p.shape[:3] != ids.shape, "payload must have shape [B,H,T,words_or_values]"
+    yield (any(t is not None and t.device != c.device for t in (ids, p, ct.metadata, ct.scale)),
+           "all cache tensors must share a device")
+    yield c.dtype != torch.float16, "centroids must be FP16"
+    yield p.dtype != lay.payload_dtype, "payload dtype does not match the compression plan"
+    yield min(ids.shape) < 1, "cache dimensions must be nonempty"
+    yield ids.dtype not in _ID_DTYPES, "cluster IDs must be integer tensors"
+    yield p.shape[-1] != lay.payload_width, "payload width does not match the compression plan"
+    m = ct.metadata
+    if lay.meta is None:
+        yield m is not None, "quantized unstructured payloads do not use sparse metadata"
+    else:
+        words, dtype = lay.meta
+        yield (m is None or tuple(m.shape) != (*ids.shape, words) or m.dtype != dtype,
+               "sparse metadata shape/dtype does not match the compression plan")
+    s = ct.scale
+    if lay.scaled:
+        yield (s is None or tuple(s.shape) != tuple(ids.shape) or s.dtype != torch.float16,
+               "quantized scales must be FP16 [B,H,T]")
+    else:
+        yield s is not None, "FP16 sparse-only caches do not use quantization scales"
+
+
+def _kernel_view(t: torch.Tensor) -> torch.Tensor:
+    """t itself when its token rows are dense and 16-byte aligned, else a contiguous copy."""
+    rows_dense = t.stride(-1) == 1 and (t.dim() == 2 or t.shape[-2] == 1 or t.stride(-2) == t.shape[-1])
     aligned = (t.storage_offset() * t.element_size()) % 16 == 0
-    return t if inner_dense and aligned else t.contiguous()
-
-
-def _check_metadata(plan: KernelPlan, metadata, shape3):
-    spec = plan.metadata_spec
-    if spec is None:
-        if metadata is not None:
-            raise ValueError("quantized unstructured payloads do not use sparse metadata")
-        return
-    words, dtype_name = spec
-    dtype = getattr(torch, dtype_name)
-    if metadata is None or tuple(metadata.shape) != (*shape3, words) or metadata.dtype != dtype:
-        raise ValueError("sparse metadata shape/dtype does not match the compression plan")
+    return t if rows_dense and aligned else t.contiguous()
 
 
 @dataclass
@@ -59,49 +101,15 @@ class CompressedTensor:
     _native: tuple = field(default=(), init=False, repr=False)
 
     def __post_init__(self):
-        c, ids, p = self.centroids, self.cluster_ids, self.payload
-        if c.ndim != 4 or c.shape[-1] != 128:
-            raise ValueError("centroids must have shape [B,H,C,128]")
-        if ids.ndim != 3 or ids.shape[:2] != c.shape[:2]:
-            raise ValueError("cluster IDs must have shape [B,H,T]")
-        if not 1 <= c.shape[2] <= 64:
-            raise ValueError("centroid count must be between 1 and 64")
-        if p.ndim != 4 or p.shape[:3] != ids.shape:
-            raise ValueError("payload must have shape [B,H,T,words_or_values]")
-        members = (c, ids, p, self.metadata, self.scale)
-        if any(t is not None and t.device != c.device for t in members):
-            raise ValueError("all cache tensors must share a device")
-        if c.dtype != torch.float16:
-            raise ValueError("centroids must be FP16")
-        want = torch.float16 if self.plan.bits == 16 else torch.int32
-        if p.dtype != want:
-            raise ValueError("payload dtype does not match the compression plan")
-        b, h, t = ids.shape
-        if min(b, h, t) < 1:
-            raise ValueError("cache dimensions must be nonempty")
-        if ids.dtype not in _ID_DTYPES:
-            raise ValueError("cluster IDs must be integer tensors")
-        if p.shape[-1] != self.plan.payload_width:
-            raise ValueError("payload width does not match the compression plan")
-        _check_metadata(self.plan, self.metadata, (b, h, t))
-        if self.plan.bits != 16:
-            s = self.scale
-            if s is None or tuple(s.shape) != (b, h, t) or s.dtype != torch.float16:
-                raise ValueError("quantized scales must be FP16 [B,H,T]")
-        elif self.scale is not None:
-            raise ValueError("FP16 sparse-only caches do not use quantization scales")
-        # int8 ids; tensors that are views into larger capacity buffers (rows of
-        # each (batch, head) block evenly strided) stay views: the kernels read
-        # them in place, and [B, H] merge into one dimension without a copy.
-        self.cluster_ids = ids if ids.dtype == torch.int8 else ids.to(torch.int8).contiguous()
-        bh = b * h
-        self._native = (
-            _rows(c.reshape(bh, -1, 128)),
-            _rows(self.cluster_ids.reshape(bh, t)),
-            _rows(p.reshape(bh, t, -1)),
-            None if self.metadata is None else _rows(self.metadata.reshape(bh, t, -1)),
-            None if self.scale is None else _rows(self.scale.reshape(bh, t)),
-        )
+        for failed, message in _violations(self):
+            if failed:
+                raise ValueError(message)
+        if self.cluster_ids.dtype != torch.int8:
+            self.cluster_ids = self.cluster_ids.to(torch.int8).contiguous()
+        b, h, t = self.cluster_ids.shape
+        flat = lambda x, *tail: None if x is None else _kernel_view(x.reshape(b * h, *tail))  # noqa: E731
+        self._native = (flat(self.centroids, -1, 128), flat(self.cluster_ids, t), flat(self.payload, t, -1),
+                        flat(self.metadata, t, -1), flat(self.scale, t))
 
     @property
     def seq_len(self) -> int:
@@ -110,41 +118,28 @@ class CompressedTensor:
     @property
     def tensors(self) -> tuple:
         """All stored tensors, including the flattened views handed to the kernels."""
-        return (self.centroids, self.cluster_ids, self.payload, self.metadata, self.scale, *self._native)
+        return (self.centroids, *(getattr(self, n) for n in _STORED), *self._native)
 
     @property
     def nbytes(self) -> int:
         return _storage_bytes(self.tensors)
 
+    def _rebuild(self, centroids, fn) -> "CompressedTensor":
+        grown = {n: (None if getattr(self, n) is None else fn(n)) for n in _STORED}
+        return CompressedTensor(centroids, grown["cluster_ids"], grown["payload"], grown["metadata"],
+                                grown["scale"], self.plan)
+
     def append(self, other: "CompressedTensor") -> "CompressedTensor":
-        """Concatenate along T, taking the newer centroid table (reskv/tensors.py:105-119)."""
+        """This history followed by ``other`` along T, with ``other``'s (newer,
+        possibly longer) centroid table (reskv/tensors.py:105-119)."""
         if self.plan != other.plan:
             raise ValueError("cannot concatenate different cache plans")
-
-        def cat(a, b):
-            return None if a is None else torch.cat((a, b), dim=2)
-
-        return CompressedTensor(
-            other.centroids,
-            cat(self.cluster_ids, other.cluster_ids),
-            cat(self.payload, other.payload),
-            cat(self.metadata, other.metadata),
-            cat(self.scale, other.scale),
-            self.plan,
-        )
+        return self._rebuild(other.centroids, lambda n: torch.cat((getattr(self, n), getattr(other, n)), dim=2))
 
     def index_select(self, index: torch.Tensor) -> "CompressedTensor":
-        def take(t):
-            return None if t is None else t.index_select(0, index.to(t.device))
-
-        return CompressedTensor(
-            take(self.centroids),
-            take(self.cluster_ids),
-            take(self.payload),
-            take(self.metadata),
-            take(self.scale),
-            self.plan,
-        )
+        """The batch rows ``index`` (beam reordering)."""
+        pick = lambda x: x.index_select(0, index.to(x.device))  # noqa: E731
+        return self._rebuild(pick(self.centroids), lambda n: pick(getattr(self, n)))
 
 
 @dataclass
@@ -168,10 +163,7 @@ class CompressedKV:
 
 
 def _storage_bytes(tensors) -> int:
-    """Bytes in unique backing storages; views of one storage count once."""
-    seen = {}
-    for t in tensors:
-        if isinstance(t, torch.Tensor):
-            storage = t.untyped_storage()
-            seen[(t.device, storage.data_ptr())] = storage.nbytes()
-    return sum(seen.values())
+    """Bytes of the distinct storages behind ``tensors`` (views share one)."""
+    storages = {(t.device, t.untyped_storage().data_ptr()): t.untyped_storage().nbytes()
+                for t in tensors if isinstance(t, torch.Tensor)}
+    return sum(storages.values())

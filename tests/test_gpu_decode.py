@@ -119,30 +119,46 @@ def test_residual_widths_through_family_ops(device, fmt, width):
         assert _max_err(out.view(b, hk * g, 1, 128), ref) <= ATOL, splits
 
 
-@pytest.mark.parametrize("bits,sparsity,layout,b,t", [(16, 0.5, "unstructured", 32, 8192),
-                                                      (16, 0.75, "structured", 32, 8192),
-                                                      (4, 0.5, "unstructured", 8, 16384),
-                                                      (2, 0.5, "unstructured", 8, 16384)])
-def test_benchmark_shapes_against_fp32_checker(device, bits, sparsity, layout, b, t):
+@pytest.mark.parametrize("bits,sparsity,layout,b,t,inputs", [(16, 0.5, "unstructured", 32, 8192, "sweep"),
+                                                             (16, 0.75, "structured", 32, 8192, "sweep"),
+                                                             (4, 0.5, "unstructured", 8, 16384, "outlier"),
+                                                             (2, 0.5, "unstructured", 8, 16384, "outlier")])
+def test_benchmark_shapes_against_fp32_checker(device, bits, sparsity, layout, b, t, inputs):
     """Configs 2 and 3 at their full shapes (Hq = 32, Hk = 8): the split-K decode at the
-    automatic split count and at 16 splits against the float32 torch reconstruction
-    (reskv_amd.reference, pinned to the oracle's golden vectors on the CPU)."""
-    from reskv_amd.reference import reference_attention
+    automatic split count and at 16 splits against the float32 torch port of the oracle
+    (oracle/torch_checker.py, pinned to the oracle's golden vectors on the CPU).
 
-    g = torch.Generator(device=device).manual_seed(7)
-    shape = (b, 8, t, 128)
-    k = torch.randn(shape, device=device, dtype=torch.float16, generator=g) * 0.5
-    v = torch.randn(shape, device=device, dtype=torch.float16, generator=g) * 0.5
-    kc = torch.randn(b, 8, 32, 128, device=device, dtype=torch.float16, generator=g) * 0.1
-    vc = torch.randn(b, 8, 32, 128, device=device, dtype=torch.float16, generator=g) * 0.1
-    ki = torch.randint(32, shape[:3], device=device, dtype=torch.int32, generator=g)
-    vi = torch.randint(32, shape[:3], device=device, dtype=torch.int32, generator=g)
-    q = torch.randn(b, 32, 1, 128, device=device, dtype=torch.float16, generator=g)
-    cfg = ResKVKernelConfig(bits=bits, sparsity=sparsity, layout=layout)
-    cache = compress(k, v, cfg, clustering=((kc, ki), (vc, vi)))
+    Config 2 uses the timing sweep's inputs (0.5 N(0,1) K and V, 0.1 N(0,1) centres,
+    random ids; reskv benchmarks/kernels.py:57-65).  Config 3 uses its own recipe:
+    outlier-channel K (N(0,1) x LogNormal(0,1) per channel, 4 channels x 10), N(0,1) V,
+    clustered by the device K-means (32 clusters, 10 iterations).  Its "group-64
+    asymmetric INT4/INT2 with fp16 scale and zero-point" resolves to the reference
+    kernel format, which is what is built and tested here: symmetric codes with one
+    fp16 scale per token and no zero-point (reskv/csrc/compression.cu:339-360,
+    decoded by reskv/reference.py:17-21); "group 64" is the decode-group token count
+    (reskv/config.py:87), not a channel group."""
+    from oracle import torch_checker as tc
+
+    if inputs == "sweep":
+        g = torch.Generator(device=device).manual_seed(7)
+        shape = (b, 8, t, 128)
+        k = torch.randn(shape, device=device, dtype=torch.float16, generator=g) * 0.5
+        v = torch.randn(shape, device=device, dtype=torch.float16, generator=g) * 0.5
+        kc = torch.randn(b, 8, 32, 128, device=device, dtype=torch.float16, generator=g) * 0.1
+        vc = torch.randn(b, 8, 32, 128, device=device, dtype=torch.float16, generator=g) * 0.1
+        ki = torch.randint(32, shape[:3], device=device, dtype=torch.int32, generator=g)
+        vi = torch.randint(32, shape[:3], device=device, dtype=torch.int32, generator=g)
+        q = torch.randn(b, 32, 1, 128, device=device, dtype=torch.float16, generator=g)
+        cfg = ResKVKernelConfig(bits=bits, sparsity=sparsity, layout=layout)
+        cache = compress(k, v, cfg, clustering=((kc, ki), (vc, vi)))
+    else:
+        k, v, q = outlier_kv(b, 8, t, seed=3)
+        cfg = ResKVKernelConfig(bits=bits, sparsity=sparsity, layout=layout, num_clusters=32, kmeans_iterations=10)
+        cache = compress(k, v, cfg)
+        assert cache.key.scale is not None and cache.key.metadata is None  # symmetric per-token codes
     del k, v
     freq = theta_freq()
-    ref = reference_attention(q, cache, position=t, inv_freq=freq)
+    ref = tc.attention(q, cache, position=t, inv_freq=freq)
     for splits in (0, 16):
         out = attention(q, cache, position=t, inv_freq=freq, splits=splits)
         err = (out.float() - ref).abs().max().item()
