@@ -13,8 +13,10 @@ call is reported next to it).  ``value`` = batch * steps / elapsed (tokens/s).
 The JSON line also carries the roofline of one decode-attention call
 (algorithmic compressed bytes per call / measured time per call vs 8 TB/s),
 a sweep over the batch sizes and sparsities of config 2 plus the dense fp16
-baseline at the same shapes, and a CPU baseline: the numpy oracle
-(reconstruct + float64 attention) on a bounded sample, timed on this host.
+baseline at the same shapes, config 1 (prefill compression), config 3
+(INT4/INT2 decode), a stated-length config-4 end-to-end decode (ResKV against
+dense fp16 KV), and a CPU baseline: the torch restatement of the reference's
+compress and attention (oracle/torch_checker.py) on this host's cores.
 """
 
 import argparse
@@ -43,8 +45,9 @@ def parse():
     p.add_argument("--splits", type=int, default=0, help="split-K count (0: automatic)")
     p.add_argument("--no-sweep", action="store_true")
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--cpu-seconds", type=float, default=12.0)
-    p.add_argument("--e2e-steps", type=int, default=2048, help="new tokens per sequence for --only e2e")
+    p.add_argument("--no-e2e", action="store_true", help="leave the config-4 end-to-end decode out of the line")
+    p.add_argument("--e2e-steps", type=int, default=256,
+                   help="new tokens per sequence timed in the config-4 decode (config 4 names 2048)")
     p.add_argument("--e2e-batch", type=int, default=16)
     p.add_argument("--e2e-prompt", type=int, default=8192)
     p.add_argument("--only", choices=("encode", "quantized", "e2e"), default=None,
@@ -314,7 +317,10 @@ def measure_e2e(torch, device, batch=16, prompt=8192, steps=2048, warmup=4, attn
     first = model.prefill(ids, sink)
     torch.cuda.synchronize()
     out = {"prefill_s_incl_compression": time.perf_counter() - t0, "batch": batch, "prompt": prompt,
-           "new_tokens": steps, "model": "random-init Llama-3.1-8B shape (fp16 weights)"}
+           "new_tokens_timed": steps, "config4_new_tokens": 2048,
+           "note": f"decode rates timed over {steps} greedy tokens after {warmup} warm-up tokens "
+                   f"(config 4 names 2048; the per-token work is the same, the history {prompt}+{steps})",
+           "model": "random-init Llama-3.1-8B shape (fp16 weights)"}
     for name, dec in decs.items():
         dec.start(first)
         dec.capture()
@@ -354,41 +360,106 @@ def _reskv_cache_mb(dec):
             "dense_fp16_same_length": 2 * dec.batch * 8 * layer.length * 128 * 2 / 1e6}
 
 
-def cpu_baseline(seconds_budget, t, sparsity):
-    """numpy oracle decode (reconstruct + float64 attention) on one batch element."""
-    import numpy as np
+def cpu_baseline():
+    """The reference's CPU path restated with torch (oracle/torch_checker.py,
+    pinned to the numpy oracle and its golden vectors): ``compress`` (K-means
+    + residual encode) and reference attention over the reconstruction, on
+    this host's cores, 1 warm-up then the median of 3.  Bounded samples:
+
+    * config 0: B = 1, 8 KV heads, T = 960 compressed (15 K-means iterations,
+      50% bitmap) + attention with 64 dense sink/recent tokens -- in full;
+    * config 1: compress of one layer, 8 heads x 8192 tokens, 10 iterations,
+      75% structured -- in full;
+    * config 2: attention at T = 8192, 50% bitmap on 4 of the 32 batch
+      elements, scaled by 8 to B = 32 (time is linear in B);
+    * config 3: attention at T = 16384, INT4 and INT2, 1 of the 8 batch
+      elements, scaled by 8.
+
+    ``value`` is the config-2 decode rate in the metric's unit: B = 32 tokens
+    per 32-layer step.
+    """
+    import statistics
+
+    import torch
 
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
-    from oracle import reskv_oracle as o
+    from oracle import torch_checker as tc
+    from reskv_amd.config import KernelPlan
+    from reskv_amd.tensors import CompressedKV, CompressedTensor
 
-    rng = np.random.default_rng(42)
-    nnz = int(128 * (1 - sparsity))
-    k = (rng.standard_normal((1, HK, t, D)) * 0.5).astype(np.float16)
-    v = (rng.standard_normal((1, HK, t, D)) * 0.5).astype(np.float16)
-    kc = (rng.standard_normal((1, HK, 32, D)) * 0.1).astype(np.float16)
-    vc = (rng.standard_normal((1, HK, 32, D)) * 0.1).astype(np.float16)
-    ki = rng.integers(0, 32, (1, HK, t))
-    vi = rng.integers(0, 32, (1, HK, t))
-    kp, km = o.encode_bitmap(k, kc, ki, nnz)
-    vp, vm = o.encode_bitmap(v, vc, vi, nnz)
-    q = rng.standard_normal((1, HQ, 1, D)).astype(np.float16)
-    f = o.theta_frequencies(500000.0)
+    cores = max(1, min(len(os.sched_getaffinity(0)), int(os.environ.get("OMP_NUM_THREADS", "16") or 16)))
+    torch.set_num_threads(cores)
+    gen = torch.Generator().manual_seed(42)
 
-    def one():
-        kd = o.reconstruct("bitmap", kc, ki, kp, km)
-        vd = o.reconstruct("bitmap", vc, vi, vp, vm)
-        o.reference_attention(q, kd, vd, position=t, freq=f)
+    def median3(fn):
+        fn()
+        runs = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            fn()
+            runs.append(time.perf_counter() - t0)
+        return statistics.median(runs)
 
-    one()
-    n, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < seconds_budget:
-        one()
-        n += 1
-    per_elem = (time.perf_counter() - t0) / n
-    return {"value": 1.0 / (LAYERS * per_elem), "unit": "tokens/s", "cores": 1, "kind": "port",
-            "sample": f"numpy oracle (single-threaded BLAS-free float64 path): reconstruct + attention for 1 batch "
-                      f"element x {HK} KV heads x T={t}, bitmap {int(sparsity * 100)}% sparsity, {n} repetitions "
-                      f"({per_elem * 1e3:.1f} ms each); tokens/s = 1 / ({LAYERS} layers x time per element)"}
+    def outlier_k(b, t):
+        scale = torch.exp(torch.randn(1, HK, 1, D, generator=gen))
+        scale[..., :4] *= 10.0
+        return (torch.randn(b, HK, t, D, generator=gen) * scale).half()
+
+    def cache_of(b, t, fmt, bits=16):
+        x = (torch.randn(b, HK, t, D, generator=gen) * 0.5).half()
+        c = (torch.randn(b, HK, 32, D, generator=gen) * 0.1).half()
+        ids = torch.randint(32, (b, HK, t), generator=gen, dtype=torch.int32)
+        if fmt == "bitmap":
+            p, m = tc.encode_bitmap(x, c, ids, 64)
+            ct = CompressedTensor(c, ids, p, m, None, KernelPlan("unstructured", "deferred", 16, 64, 2, 0))
+        else:
+            p, sc = tc.encode_multibit(x, c, ids, 64, bits)
+            ct = CompressedTensor(c, ids, p, None, sc, KernelPlan("unstructured", "per_token", bits, 64, 16, 0))
+        return CompressedKV(ct, ct)
+
+    out = {}
+    # config 0
+    k0, v0 = outlier_k(1, 1024), torch.randn(1, HK, 1024, D, generator=gen).half()
+    q0 = torch.randn(1, HQ, 1, D, generator=gen).half()
+    kc, vc = k0[:, :, 4:964].contiguous(), v0[:, :, 4:964].contiguous()
+
+    def c0_compress():
+        (a, ai), (b_, bi) = tc.kmeans(kc, 32, 15), tc.kmeans(vc, 32, 15, value=True)
+        return tc.encode_bitmap(kc, a, ai, 64), tc.encode_bitmap(vc, b_, bi, 64), (a, ai, b_, bi)
+
+    (kp, km), (vp, vm), (a, ai, b_, bi) = c0_compress()
+    plan = KernelPlan("unstructured", "deferred", 16, 64, 2, 0)
+    cache0 = CompressedKV(CompressedTensor(a, ai, kp, km, None, plan), CompressedTensor(b_, bi, vp, vm, None, plan))
+    recent = (q0, k0[:, :, list(range(4)) + list(range(964, 1024))], v0[:, :, list(range(4)) + list(range(964, 1024))])
+    out["config0"] = {"compress_s": median3(c0_compress),
+                      "attention_s": median3(lambda: tc.attention(q0, cache0, position=1024, start_position=4,
+                                                                  recent=recent))}
+    # config 1
+    k1, v1 = outlier_k(1, 8192), torch.randn(1, HK, 8192, D, generator=gen).half()
+
+    def c1_compress():
+        (a, ai), (b_, bi) = tc.kmeans(k1, 32, 10), tc.kmeans(v1, 32, 10, value=True)
+        tc.encode_structured(k1, a, ai, 32)
+        tc.encode_structured(v1, b_, bi, 32)
+
+    out["config1"] = {"compress_s": median3(c1_compress)}
+    # config 2 (4 of 32 batch elements)
+    cache2 = cache_of(4, T, "bitmap")
+    q2 = torch.randn(4, HQ, 1, D, generator=gen).half()
+    per_call = median3(lambda: tc.attention(q2, cache2, position=T)) * 8
+    out["config2_b32_s50"] = {"attention_s_per_layer_step": per_call, "sample": "4 of 32 batch elements, x8"}
+    # config 3 (1 of 8 batch elements)
+    for bits in (4, 2):
+        cache3 = cache_of(1, 16384, "quant", bits)
+        q3 = torch.randn(1, HQ, 1, D, generator=gen).half()
+        out[f"config3_int{bits}"] = {"attention_s_per_layer_step": median3(
+            lambda: tc.attention(q3, cache3, position=16384)) * 8, "sample": "1 of 8 batch elements, x8"}
+        del cache3
+    return {"value": 32 / (LAYERS * per_call), "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": "torch CPU restatement of compress + reference attention (oracle/torch_checker.py), "
+                      f"{cores} threads, 1 warm-up + median of 3 per item; value = config 2 (B=32, T=8192, "
+                      "50% bitmap) decode tokens/s from 4 of 32 batch elements scaled x8, 32 layers per step",
+            "configs": out}
 
 
 def measured_traffic(b, t, sparsity, layout):
@@ -416,9 +487,6 @@ def main():
         print(json.dumps({"error": "this build runs on one GPU; multi-GPU sharding is a design note only, "
                                    "so --gpus above 1 is not supported", "n_gpus": args.gpus}))
         sys.exit(2)
-    # keep numpy's CPU baseline single-threaded so `cores` is what was used
-    for var in ("OMP_NUM_THREADS", "OPENBLAS_NUM_THREADS", "MKL_NUM_THREADS"):
-        os.environ[var] = "1"
     import torch
 
     if not torch.cuda.is_available():
@@ -468,7 +536,11 @@ def main():
     dense_b = next((d for d in dense if d["batch"] == args.batch), None)
     if dense_b is None:
         dense_b = measure_dense(torch, args.batch, args.seq_len, args.layers, max(5, args.steps // 2), 2, device)
-    cpu = None if args.no_cpu_baseline else cpu_baseline(args.cpu_seconds, args.seq_len, args.sparsity)
+    e2e = None
+    if not args.no_e2e:
+        e2e = measure_e2e(torch, device, args.e2e_batch, args.e2e_prompt, args.e2e_steps)
+        print(json.dumps({"e2e": e2e}), flush=True)
+    cpu = None if args.no_cpu_baseline else cpu_baseline()
     traffic = measured_traffic(args.batch, args.seq_len, args.sparsity, r["layout"])
     secs = r["seconds"]
     line = {
@@ -482,14 +554,18 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp32",
+        "dtype": "fp32+fp16",
         "data": "synthetic",
         "config": {
             "workload": f"config 2 compressed-KV decode attention, one decode step = {args.layers} layer calls "
                         f"(graph-replayed), batch {args.batch}, T={args.seq_len}, sparsity {args.sparsity}",
             "batch": args.batch, "seq_len": args.seq_len, "q_heads": HQ, "kv_heads": HK, "head_dim": D,
             "sparsity": args.sparsity, "layout": r["layout"], "centroid_fusion": r["fusion"],
-            "splits": r["splits"], "storage": "fp16 residuals + int8 ids, fp32 arithmetic",
+            "splits": r["splits"],
+            "storage": "fp16 centroids and residuals, int8 cluster ids, int64 bitmaps",
+            "arithmetic": "fp32 RoPE, scores (v_mfma_f32_4x4x1f32) and online softmax; the softmax weights "
+                          "are rounded to fp16 for P x V and the cluster mass on v_mfma_f32_4x4x4f16 with "
+                          "fp32 accumulation",
             "attn_us_per_layer_step": r["us_per_layer_step"],
             "eager_us_per_layer_step": r["eager_us_per_layer_step"],
             "dense_fp16_us_per_layer_step": dense_b["us_per_layer_step"],
@@ -499,6 +575,7 @@ def main():
             "dense_sweep": [{k: d[k] for k in ("batch", "us_per_layer_step", "frac")} for d in dense],
             "config1_prefill_compression": encode,
             "config3_quantized_decode_b8_t16384": quant,
+            "config4_end_to_end": e2e,
         },
         "roofline": {
             "bound": "hbm", "achieved": r["achieved_GBps"], "peak": HBM_PEAK / 1e9, "unit": "GB/s",

@@ -109,3 +109,99 @@ def attention(query, cache, *, position, start_position=0, inv_freq=None, rope_t
         scores = torch.cat((scores, torch.matmul(qr, kr.repeat_interleave(g, 1).transpose(-1, -2)) * scale), -1)
         v = torch.cat((v, vr.repeat_interleave(g, 1)), dim=2)
     return torch.matmul(torch.softmax(scores, dim=-1), v)
+
+
+# ---------------------------------------------------------------------------
+# compress, for the CPU baseline: the numpy oracle's kmeans and encoders on
+# torch tensors (any device), so that bench.py can time a multi-threaded CPU
+# restatement of compress (reskv/compression.py:19-101).  Pinned against the
+# numpy oracle by tests/test_torch_checker.py.
+# ---------------------------------------------------------------------------
+
+def _fp16_sqrt(d16):
+    return d16.double().clamp_min(0).sqrt().half()
+
+
+def kmeans(x, count, iterations, *, value=False):
+    """Lloyd k-means per (batch, head) on x fp16 [B, H, T, 128] (T >= count).
+
+    K: fp32 data and distances (|x|^2 + |c|^2 - 2 x.c), empty clusters keep
+    their centre; V: the fp16 cdist rule (fp16 norms, fp16 distance, fp16
+    root, lowest index on ties), fp16 centres, empty -> 0.  Returns (centres
+    fp16 [B, H, C, 128], ids int32 [B, H, T]) as reskv_oracle.kmeans.
+    """
+    b, h, t, _ = x.shape
+    count = min(count, t) if value else count
+    rows = x.reshape(b * h, t, D)
+    idx = torch.linspace(0, t - 1, count).long()
+    data = rows.float()
+    centres = data[:, idx].clone()
+    if value:
+        xn = (rows.float() * rows.float()).half().float().sum(-1).half().float()
+    for _ in range(iterations):
+        if value:
+            c16 = centres.half()
+            cn = (c16.float() * c16.float()).half().float().sum(-1).half().float()
+            dot = torch.bmm(data.double(), c16.double().transpose(1, 2))
+            d16 = (xn.double()[..., None] + cn.double()[:, None, :] - 2.0 * dot).half()
+            ids = _fp16_sqrt(d16).float().argmin(-1)
+        else:
+            d = (data * data).sum(-1, keepdim=True) - 2.0 * torch.bmm(data, centres.transpose(1, 2)) \
+                + (centres * centres).sum(-1)[:, None, :]
+            ids = d.argmin(-1)
+        onehot = torch.nn.functional.one_hot(ids, count).float()
+        counts = onehot.sum(1)[..., None]
+        sums = torch.bmm(onehot.transpose(1, 2), data)
+        mean = sums / counts.clamp_min(1)
+        centres = mean.half().float() if value else torch.where(counts > 0, mean, centres)
+    return centres.reshape(b, h, count, D).half(), ids.reshape(b, h, t).int()
+
+
+def _residual_and_key(x, centres, ids):
+    cent = centres.gather(2, ids.long().clamp(0, centres.shape[2] - 1)[..., None].expand(*ids.shape, D))
+    r = x.float() - cent.float()
+    return r, r.half().float().abs()
+
+
+def _top_mask(key, k):
+    """k largest keys per row, lowest index on ties (a stable descending sort)."""
+    order = torch.sort(key, dim=-1, descending=True, stable=True).indices[..., :k]
+    return torch.zeros_like(key, dtype=torch.bool).scatter_(-1, order, True)
+
+
+def encode_bitmap(x, centres, ids, nnz):
+    """Unstructured FP16: payload fp16 [..., nnz] ascending, int64 MSB-first bitmaps [..., 2]."""
+    r, key = _residual_and_key(x, centres, ids)
+    mask = _top_mask(key, nnz)
+    payload = r.half()[mask].reshape(*mask.shape[:-1], nnz)
+    bits = mask.reshape(*mask.shape[:-1], 2, 64).long()
+    words = (bits << torch.arange(63, -1, -1)).sum(-1)  # int64 wraps like the reference's bit 63
+    return payload, words
+
+
+def encode_structured(x, centres, ids, nnz=32):
+    """Tiled / structured 4:16 FP16 with four-nibble codes: payload [..., nnz], int32 words [..., 4]."""
+    per_tile = nnz // 8
+    r, key = _residual_and_key(x, centres, ids)
+    tiles = key.reshape(*key.shape[:-1], 8, 16)
+    mask = _top_mask(tiles, per_tile)
+    payload = r.half()[mask.reshape(*mask.shape[:-2], D)].reshape(*mask.shape[:-2], nnz)
+    pos = torch.sort(torch.sort(tiles, dim=-1, descending=True, stable=True).indices[..., :per_tile], dim=-1).values
+    codes = (pos.long() << (4 * torch.arange(per_tile))).sum(-1)
+    words = (codes[..., 0::2] | (codes[..., 1::2] << 16)) & 0xFFFFFFFF
+    return payload, (words - ((words >> 31) << 32)).to(torch.int32)  # as signed int32 words
+
+
+def encode_multibit(x, centres, ids, nnz, bits):
+    """Top-nnz + symmetric INT4/INT2 codes with an fp16 per-token scale."""
+    qmax = (1 << (bits - 1)) - 1
+    per_word = 32 // bits
+    r, key = _residual_and_key(x, centres, ids)
+    mask = _top_mask(key, nnz)
+    amax = torch.where(mask, r.abs(), torch.zeros(())).amax(-1)
+    scale = torch.where(amax > 0, (amax / qmax).half(), torch.ones((), dtype=torch.float16))
+    q = torch.clamp(torch.round(r / scale.float()[..., None]), -qmax, qmax).long()
+    q = torch.where(mask, q, torch.zeros((), dtype=torch.long)) & ((1 << bits) - 1)
+    q = q.reshape(*q.shape[:-1], D // per_word, per_word)
+    words = (q << (torch.arange(per_word) * bits)).sum(-1)
+    return (words - ((words >> 31) << 32)).to(torch.int32), scale  # as signed int32 words

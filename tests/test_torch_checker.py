@@ -70,3 +70,57 @@ def test_checker_reconstruction_equals_the_oracle(key):
                             meta, scale, bits=bits)
         got = tc.reconstruct(ct).double().numpy()
         assert np.abs(got - ref).max() <= 1e-6 * max(1.0, np.abs(ref).max())
+
+
+# ---------------------------------------------------------------------------
+# the torch restatement of compress (used only by bench.py's CPU baseline)
+# ---------------------------------------------------------------------------
+
+def _inputs(seed, b=1, h=2, t=300):
+    g = torch.Generator().manual_seed(seed)
+    x = (torch.randn(b, h, t, 128, generator=g) * torch.exp(torch.randn(1, h, 1, 128, generator=g))).half()
+    c = (torch.randn(b, h, 16, 128, generator=g) * 0.3).half()
+    ids = torch.randint(16, (b, h, t), generator=g, dtype=torch.int32)
+    return x, c, ids
+
+
+@pytest.mark.parametrize("nnz", [64, 32])
+def test_torch_bitmap_encoder_equals_the_oracle(nnz):
+    from oracle import reskv_oracle as o
+
+    x, c, ids = _inputs(1)
+    p, m = tc.encode_bitmap(x, c, ids, nnz)
+    ep, em = o.encode_bitmap(x.numpy(), c.numpy(), ids.numpy(), nnz)
+    assert np.array_equal(p.numpy(), ep) and np.array_equal(m.numpy(), em)
+
+
+def test_torch_structured_encoder_equals_the_oracle():
+    from oracle import reskv_oracle as o
+
+    x, c, ids = _inputs(2)
+    p, m = tc.encode_structured(x, c, ids, 32)
+    ep, em = o.encode_qtile(x.numpy(), c.numpy(), ids.numpy(), 32, True)
+    assert np.array_equal(p.numpy(), ep) and np.array_equal(m.numpy(), em)
+
+
+@pytest.mark.parametrize("bits", [4, 2])
+def test_torch_multibit_encoder_equals_the_oracle(bits):
+    from oracle import reskv_oracle as o
+
+    x, c, ids = _inputs(3)
+    q, s = tc.encode_multibit(x, c, ids, 64, bits)
+    eq, es = o.encode_multibit(x.numpy(), c.numpy(), ids.numpy(), 64, bits)
+    assert np.array_equal(s.numpy(), es)
+    assert (q.numpy() == eq).mean() > 0.999  # torch.round and numpy rint agree except on fp32 division ties
+
+
+@pytest.mark.parametrize("value", [False, True])
+def test_torch_kmeans_equals_the_oracle(value):
+    from oracle import reskv_oracle as o
+
+    x, _, _ = _inputs(4, t=600)
+    c, ids = tc.kmeans(x, 16, 3, value=value)
+    ec, eids, _ = o.kmeans(x.numpy(), 16, 3, value=value)
+    assert (ids.numpy() == eids).mean() > 0.995
+    if np.array_equal(ids.numpy(), eids):
+        assert np.abs(c.float().numpy() - ec.astype(np.float32)).max() <= 2e-2
