@@ -13,6 +13,9 @@ LIB_PATH = _HERE / "libreskv_hip.so"
 
 _vp, _i, _i64, _f = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float
 
+# reskv_abi_version() of the library these signatures describe
+ABI_VERSION = 3
+
 
 class CTensor(ctypes.Structure):
     """Mirror of ``reskv_ctensor``."""
@@ -82,6 +85,10 @@ def lib():
                     fn = getattr(handle, name)
                     fn.restype = res
                     fn.argtypes = args
+                found = handle.reskv_abi_version()
+                if found != ABI_VERSION:
+                    raise RuntimeError(f"{LIB_PATH.name} has ABI version {found}, this binding needs "
+                                       f"{ABI_VERSION}; rebuild with `python -m reskv_amd.build`")
                 _lib = handle
     return _lib
 

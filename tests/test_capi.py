@@ -32,7 +32,15 @@ def test_library_exports_every_declared_symbol():
     for name in declared_functions():
         assert hasattr(lib, name), name
         assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
-    assert lib.reskv_abi_version() == 3
+    assert lib.reskv_abi_version() == _lib.ABI_VERSION == 3
+
+
+def test_a_library_of_another_abi_version_is_refused(monkeypatch):
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(_lib, "ABI_VERSION", 2)
+    with pytest.raises(RuntimeError, match="ABI version 3, this binding needs 2"):
+        _lib.lib()
+    assert _lib._lib is None  # nothing half-loaded is kept
 
 
 def _err(status):
