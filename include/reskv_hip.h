@@ -30,7 +30,8 @@ extern "C" {
 /* Thread-local description of the last failure; "" when none. */
 const char* reskv_last_error(void);
 
-/* Library ABI version (bumped on any signature or struct change); 3. */
+/* Library ABI version (bumped on any signature or struct change, or when
+ * entry points are added); 4. */
 int reskv_abi_version(void);
 
 /* ------------------------------------------------------------------ *
@@ -52,6 +53,19 @@ int reskv_compress_fp16(const void* keys, const void* centroids, const int32_t* 
 int reskv_compress_bitmap(const void* keys, const void* centroids, const int32_t* ids,
                           void* payload, int64_t* meta, int B, int H, int T, int C,
                           int nnz, void* stream);
+
+/* A layer's K and V through reskv_compress_fp16 / reskv_compress_bitmap in
+ * one launch.  Replaces the two _encode calls of compress
+ * (reskv/compression.py:166-167), K then V with one plan; each result equals
+ * the single-tensor call's.  Ck, Cv: the two centroid counts. */
+int reskv_compress_fp16_kv(const void* k, const void* v, const void* k_centroids, const void* v_centroids,
+                           const int32_t* k_ids, const int32_t* v_ids, void* k_payload, void* v_payload,
+                           int32_t* k_meta, int32_t* v_meta, int B, int H, int T, int Ck, int Cv, int nnz,
+                           int struct_index, void* stream);
+int reskv_compress_bitmap_kv(const void* k, const void* v, const void* k_centroids, const void* v_centroids,
+                             const int32_t* k_ids, const int32_t* v_ids, void* k_payload, void* v_payload,
+                             int64_t* k_meta, int64_t* v_meta, int B, int H, int T, int Ck, int Cv, int nnz,
+                             void* stream);
 
 /* Unstructured top-nnz + symmetric INT4/INT2 quantiser.
  * Replaces ext.compress_quantized (reskv/csrc/compression.cu:392-421, op at :510).

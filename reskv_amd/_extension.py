@@ -180,6 +180,41 @@ def compress_bitmap(keys, centroids, cluster_ids, nnz_per_token):
     return [payload, meta]
 
 
+def _check_pair(k, kc, ki, v, vc, vi):
+    b, h, t, ck = _check_encoder_inputs(k, kc, ki)
+    cv = _check_encoder_inputs(v, vc, vi)[3]
+    _require(tuple(v.shape) == tuple(k.shape) and v.device == k.device, "K and V must have identical shapes and devices")
+    return b, h, t, ck, cv
+
+
+def compress_fp16_kv(k, k_centroids, k_ids, v, v_centroids, v_ids, nnz_per_token, use_4x16_struct_index):
+    """``compress_fp16`` of a layer's K and of its V in one launch
+    (reskv/compression.py:166-167).  Returns ((payload, meta) of K, of V)."""
+    b, h, t, ck, cv = _check_pair(k, k_centroids, k_ids, v, v_centroids, v_ids)
+    nnz, dev = int(nnz_per_token), k.device
+    out = [(_empty((b, h, t, nnz), torch.float16, dev), _empty((b, h, t, 4), torch.int32, dev)) for _ in range(2)]
+    with torch.cuda.device(dev):
+        _lib.check(_lib.lib().reskv_compress_fp16_kv(
+            k.data_ptr(), v.data_ptr(), k_centroids.data_ptr(), v_centroids.data_ptr(), k_ids.data_ptr(),
+            v_ids.data_ptr(), out[0][0].data_ptr(), out[1][0].data_ptr(), out[0][1].data_ptr(), out[1][1].data_ptr(),
+            b, h, t, ck, cv, nnz, int(bool(use_4x16_struct_index)), _stream(dev)), "compress_fp16_kv")
+    return out
+
+
+def compress_bitmap_kv(k, k_centroids, k_ids, v, v_centroids, v_ids, nnz_per_token):
+    """``compress_bitmap`` of a layer's K and of its V in one launch
+    (reskv/compression.py:166-167).  Returns ((payload, meta) of K, of V)."""
+    b, h, t, ck, cv = _check_pair(k, k_centroids, k_ids, v, v_centroids, v_ids)
+    nnz, dev = int(nnz_per_token), k.device
+    out = [(_empty((b, h, t, nnz), torch.float16, dev), _empty((b, h, t, 2), torch.int64, dev)) for _ in range(2)]
+    with torch.cuda.device(dev):
+        _lib.check(_lib.lib().reskv_compress_bitmap_kv(
+            k.data_ptr(), v.data_ptr(), k_centroids.data_ptr(), v_centroids.data_ptr(), k_ids.data_ptr(),
+            v_ids.data_ptr(), out[0][0].data_ptr(), out[1][0].data_ptr(), out[0][1].data_ptr(), out[1][1].data_ptr(),
+            b, h, t, ck, cv, nnz, _stream(dev)), "compress_bitmap_kv")
+    return out
+
+
 def compress_quantized(keys, centroids, cluster_ids, nnz_per_token, bitwidth):
     """Unstructured top-nnz + signed INT4/INT2 (reskv/csrc/compression.cu:392-421)."""
     b, h, t, c = _check_encoder_inputs(keys, centroids, cluster_ids)
@@ -579,6 +614,7 @@ def _make_attention(plan):
 def _make_compression():
     return SimpleNamespace(compress_fp16=compress_fp16, compress_quantized=compress_quantized,
                            compress_structured_int4=compress_structured_int4, compress_bitmap=compress_bitmap,
+                           compress_fp16_kv=compress_fp16_kv, compress_bitmap_kv=compress_bitmap_kv,
                            kmeans=kmeans, kmeans_kv=kmeans_kv, kmeans_assign=kmeans_assign)
 
 

@@ -14,7 +14,7 @@ LIB_PATH = _HERE / "libreskv_hip.so"
 _vp, _i, _i64, _f = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float
 
 # reskv_abi_version() of the library these signatures describe
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 
 class CTensor(ctypes.Structure):
@@ -43,6 +43,8 @@ SIGNATURES = {
     "reskv_abi_version": (_i, []),
     "reskv_compress_fp16": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp]),
     "reskv_compress_bitmap": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp]),
+    "reskv_compress_fp16_kv": (_i, [_vp] * 10 + [_i] * 7 + [_vp]),
+    "reskv_compress_bitmap_kv": (_i, [_vp] * 10 + [_i] * 6 + [_vp]),
     "reskv_compress_quantized": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp]),
     "reskv_compress_structured_int4": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
     "reskv_kmeans_workspace_bytes": (_i64, [_i, _i, _i]),

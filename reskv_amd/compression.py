@@ -113,6 +113,22 @@ def _encode(x, centers, ids, plan, *, value=False):
     return CompressedTensor(centers, ids, payload, metadata, scale, plan)
 
 
+def _encode_kv(key, value, k_clusters, v_clusters, plan):
+    """``(_encode(key, ...), _encode(value, ..., value=True))``; the FP16
+    formats run K and V in one launch (reskv/compression.py:166-167)."""
+    (kc, ki), (vc, vi) = k_clusters, v_clusters
+    if plan.bits != 16:
+        return _encode(key, kc, ki, plan), _encode(value, vc, vi, plan, value=True)
+    ops = _ops(key)
+    kx, kc, ki = key.contiguous(), kc.half().contiguous(), ki.int().contiguous()
+    vx, vc, vi = value.contiguous(), vc.half().contiguous(), vi.int().contiguous()
+    if plan.layout == "unstructured":
+        (kp, km), (vp, vm) = ops.compress_bitmap_kv(kx, kc, ki, vx, vc, vi, plan.nnz)
+    else:
+        (kp, km), (vp, vm) = ops.compress_fp16_kv(kx, kc, ki, vx, vc, vi, plan.nnz, plan.layout == "structured")
+    return CompressedTensor(kc, ki, kp, km, None, plan), CompressedTensor(vc, vi, vp, vm, None, plan)
+
+
 # ---------------------------------------------------------------------------
 # compress: argument rules, then one of three clustering sources
 # ---------------------------------------------------------------------------
@@ -193,8 +209,8 @@ def compress(
         _enforce(_previous_rules(previous, key, config))
         if clustering is not None:
             raise ValueError("provide clustering or previous, not both")
-    (kc, ki), (vc, vi) = _clusters(key, value, config, previous, clustering)
-    k, v = _encode(key, kc, ki, plan), _encode(value, vc, vi, plan, value=True)
+    k_clusters, v_clusters = _clusters(key, value, config, previous, clustering)
+    k, v = _encode_kv(key, value, k_clusters, v_clusters, plan)
     if previous is not None:
         return CompressedKV(previous.key.append(k), previous.value.append(v))
     return CompressedKV(k, v)
@@ -204,5 +220,5 @@ def _compress_group(key, value, config, previous, plan):
     """One decode group against the shared centroid tables of ``previous``:
     the group's own K and V CompressedTensors, each carrying the extended
     centroid table (the device cache appends them in place)."""
-    (kc, ki), (vc, vi) = _clusters(key, value, config, previous, None)
-    return _encode(key, kc, ki, plan), _encode(value, vc, vi, plan, value=True)
+    k_clusters, v_clusters = _clusters(key, value, config, previous, None)
+    return _encode_kv(key, value, k_clusters, v_clusters, plan)

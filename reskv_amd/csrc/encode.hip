@@ -16,6 +16,18 @@ namespace {
 
 constexpr int kWavesPerBlock = 4;
 
+// The tensors one launch encodes: side 0 and, for a layer's K and V in one
+// launch, side 1 (grid dimension y for the 4:16 encoder, z for the bitmap
+// encoder selects the side).
+struct EncSides {
+    const uint16_t* x[2];     // tokens fp16 [B*H*T, 128]
+    const uint16_t* cent[2];  // centroids fp16 [B*H, C, 128]
+    const int32_t* ids[2];    // cluster ids [B*H*T]
+    uint16_t* payload[2];
+    void* meta[2];
+    int C[2];
+};
+
 struct Residual {
     float r0, r1;     // channels L, L+64
     uint32_t m0, m1;  // |fp16(r)| as 15-bit integers (order == value order)
@@ -154,10 +166,14 @@ __device__ __forceinline__ void merge_top4(uint32_t* a, const uint32_t* b) {
     a[3] = c3;
 }
 
-__global__ void __launch_bounds__(256) encode_tile4_kernel(
-    const uint16_t* __restrict__ keys, const uint16_t* __restrict__ cent,
-    const int32_t* __restrict__ ids, uint16_t* __restrict__ payload, int32_t* __restrict__ meta,
-    long rows, int T, int C, int struct_index) {
+__global__ void __launch_bounds__(256) encode_tile4_kernel(EncSides S, long rows, int T, int struct_index) {
+    const int side = blockIdx.y;
+    const uint16_t* __restrict__ keys = S.x[side];
+    const uint16_t* __restrict__ cent = S.cent[side];
+    const int32_t* __restrict__ ids = S.ids[side];
+    uint16_t* __restrict__ payload = S.payload[side];
+    int32_t* __restrict__ meta = static_cast<int32_t*>(S.meta[side]);
+    const int C = S.C[side];
     const int lane = threadIdx.x & 63;
     const long row = ((long)blockIdx.x * 4 + (threadIdx.x >> 6)) * 8 + (lane >> 3);
     const int tile = lane & 7;
@@ -227,105 +243,201 @@ __global__ void __launch_bounds__(256) encode_bitmap_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Unstructured top-nnz with MSB-first bitmaps, eight lanes per token (lane
-// 8 t + j owns channels 16 j .. 16 j + 15 of token t).  The nnz-th largest
-// magnitude M comes from a 15-step search over the fp16 magnitude bits; each
-// step counts the token's magnitudes below the candidate with packed 16-bit
-// subtractions (sign bits gathered into one popcount) and three lane sums.
-// Channels above M are kept, and the lowest-indexed channels equal to M fill
-// the remainder (ties go to the lower channel, as with the composite key).
+// Unstructured top-nnz with MSB-first bitmaps, four lanes per token (lane
+// 4 t + q owns channels 32 q .. 32 q + 31 of token t; a wave encodes 16
+// tokens).  The nnz-th largest 15-bit magnitude M is found bit by bit on byte
+// planes: a lane's 32 magnitudes are split into a plane of high bytes (bits
+// 14..8) and one of low bytes, four values per dword, byte k of dword i
+// holding channel 32 q + 4 i + k.  For byte values v, c <= 0x80,
+// ((v | 0x80) - c) & 0x80 is set exactly when v >= c and no borrow crosses a
+// byte, so one subtraction, one mask and one popcount count four values
+// against a candidate.  Phases:
+//   A: the high seven bits H of M over the high bytes;
+//   B: bits 7..1 of M (L) over the low bytes >> 1 of the values whose high
+//      byte is H (the others read as 0 and never count: candidates are >= 1),
+//      on top of the count of values whose high byte exceeds H;
+//   C: bit 0 of M over the values whose high byte is H and low bits 7..1 are L.
+// Each step's count is summed over the token's four lanes (one quad) with two
+// DPP adds.  Channels above M are kept, and the lowest-indexed channels equal
+// to M fill the remainder (ties go to the lower channel, as with the
+// composite key).  The kept values are compacted into the wave's LDS rows and
+// written to the payload as 16-byte stores.
 // ---------------------------------------------------------------------------
-// Number of the lane's 16 magnitudes (packed pairs mp) below cand.
-__device__ __forceinline__ int count_below(const uint32_t* mp, uint32_t cand) {
-    const uint32_t cc = cand | (cand << 16);
-    uint32_t w[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        // sign bit of each 16-bit difference: set where the magnitude is below cand
-        const uint32_t d0 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(short2_t, mp[2 * i]) - __builtin_bit_cast(short2_t, cc));
-        const uint32_t d1 = __builtin_bit_cast(uint32_t, __builtin_bit_cast(short2_t, mp[2 * i + 1]) - __builtin_bit_cast(short2_t, cc));
-        w[i] = __builtin_amdgcn_perm(d1, d0, 0x07050301u);  // the four high bytes
-    }
-    const uint32_t g = (w[0] & 0x80808080u) | ((w[1] >> 1) & 0x40404040u) | ((w[2] >> 2) & 0x20202020u) |
-                       ((w[3] >> 3) & 0x10101010u);
-    return __builtin_popcount(g);
-}
-// Sum over the 8 lanes of the lane's token (lanes 8t .. 8t+7), in every one of them.
-__device__ __forceinline__ int token_sum8(int v) {
-    v += (int)dpp_u<0xB1>((uint32_t)v);   // quad xor 1
-    v += (int)dpp_u<0x4E>((uint32_t)v);   // quad xor 2
-    v += (int)dpp_u<0x141>((uint32_t)v);  // half-row mirror: the other quad of the 8
+constexpr uint32_t kByteTop = 0x80808080u;  // bit 7 of every byte
+constexpr uint32_t kByteOne = 0x01010101u;
+constexpr int kBitmapTokensPerWave = 16;
+constexpr int kBitmapDump = kBitmapTokensPerWave * kDim;  // per-wave LDS halves before the lanes' dump slots
+
+// Sum over the four lanes of the lane's token (one DPP quad), in every one of them.
+__device__ __forceinline__ int quad_sum(int v) {
+    v += (int)dpp_u<0xB1>((uint32_t)v);  // quad xor 1
+    v += (int)dpp_u<0x4E>((uint32_t)v);  // quad xor 2
     return v;
 }
-// Exclusive prefix sum over the lanes of the token, in channel order.
-__device__ __forceinline__ int token_prefix8(int v, int j) {
-    int x = v;
+// Exclusive prefix sum over the quad, in lane (channel) order.
+__device__ __forceinline__ int quad_prefix(int v, int q) {
+    int s = v;
+    const int a = (int)dpp_u<0x90>((uint32_t)s);  // quad_perm [0,0,1,2]: lane q - 1
+    s += q >= 1 ? a : 0;
+    const int b = (int)dpp_u<0x44>((uint32_t)s);  // quad_perm [0,1,0,1]: lane q - 2
+    s += q >= 2 ? b : 0;
+    return s - v;
+}
+// Bit-7 flags of the bytes of p (each ORed with 0x80 beforehand) that are >= the bytes of c4.
+__device__ __forceinline__ uint32_t ge_flags(uint32_t p, uint32_t c4) { return (p - c4) & kByteTop; }
+// Number of the lane's 32 plane bytes >= the bytes of c4.
+__device__ __forceinline__ int count_ge(const uint32_t* p, uint32_t c4) {
+    int n = 0;
 #pragma unroll
-    for (int sh = 1; sh < 8; sh <<= 1) {
-        const int o = __shfl_up(x, sh, 8);
-        x += j >= sh ? o : 0;
+    for (int i = 0; i < 8; ++i) n += __builtin_popcount(ge_flags(p[i], c4));
+    return n;
+}
+// Largest 7-bit c (as four equal bytes) with base + (token count of plane bytes >= c) >= nnz.
+__device__ __forceinline__ uint32_t search7(const uint32_t* p, int base, int nnz) {
+    uint32_t c4 = 0;
+#pragma unroll
+    for (int bit = 6; bit >= 0; --bit) {
+        const uint32_t cand = c4 | (kByteOne << bit);
+        c4 = base + quad_sum(count_ge(p, cand)) >= nnz ? cand : c4;
     }
-    return x - v;
+    return c4;
+}
+// Bit-7 flags of 4 bytes -> 4 bits in byte order.
+__device__ __forceinline__ uint32_t movemask4(uint32_t f) {
+    uint32_t t = f >> 7;  // bits 0, 8, 16, 24
+    t |= t >> 7;          // bits 0, 1 hold bytes 0, 1; bits 16, 17 hold bytes 2, 3
+    t |= t >> 14;
+    return t & 0xFu;
 }
 
-__global__ void __launch_bounds__(256) encode_bitmap8_kernel(
-    const uint16_t* __restrict__ keys, const uint16_t* __restrict__ cent,
-    const int32_t* __restrict__ ids, uint16_t* __restrict__ payload, int64_t* __restrict__ meta,
-    long rows, int T, int C, int nnz) {
-    const int lane = threadIdx.x & 63;
-    const long row = ((long)blockIdx.x * 4 + (threadIdx.x >> 6)) * 8 + (lane >> 3);
-    const int tile = lane & 7;
-    if (row >= rows) return;
-    const long bh = row / T;
+__global__ void __launch_bounds__(256) encode_bitmap4_kernel(EncSides S, int T, int nnz, int bh0) {
+    __shared__ __align__(16) uint16_t s_rows[kWavesPerBlock][kBitmapDump + kWave];
+    const int side = blockIdx.z;
+    const uint16_t* __restrict__ keys = S.x[side];
+    const uint16_t* __restrict__ cent = S.cent[side];
+    const int32_t* __restrict__ ids = S.ids[side];
+    uint16_t* __restrict__ payload = S.payload[side];
+    int64_t* __restrict__ meta = static_cast<int64_t*>(S.meta[side]);
+    const int C = S.C[side];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int q = lane & 3;
+    const int t_wave = blockIdx.x * (kWavesPerBlock * kBitmapTokensPerWave) + wave * kBitmapTokensPerWave;
+    if (t_wave >= T) return;  // whole waves
+    const int t = t_wave + (lane >> 2);
+    const bool valid = t < T;  // lanes past T compute on the last token and store nothing
+    const long bh = (long)bh0 + blockIdx.y;
+    const long row = bh * T + (valid ? t : T - 1);
     int cid = ids[row];
     cid = cid < 0 ? 0 : (cid > C - 1 ? C - 1 : cid);  // compression.cu:83-84
-    const uint4* xp = reinterpret_cast<const uint4*>(keys + row * kDim + tile * 16);
-    const uint4* cp = reinterpret_cast<const uint4*>(cent + (bh * C + cid) * kDim + tile * 16);
-    const uint4 xa = xp[0], xb = xp[1], ca = cp[0], cb = cp[1];
-    const uint32_t xw[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
-    const uint32_t cw[8] = {ca.x, ca.y, ca.z, ca.w, cb.x, cb.y, cb.z, cb.w};
-    uint32_t hp[8], mp[8];  // fp16 residual pairs, their magnitudes
+    const uint4* xp = reinterpret_cast<const uint4*>(keys + row * kDim + q * 32);
+    const uint4* cp = reinterpret_cast<const uint4*>(cent + (bh * C + cid) * kDim + q * 32);
+    uint32_t hp[16];  // fp16 residual pairs (channels 32 q + 2 i, + 1)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint4 xv = xp[j], cv = cp[j];
+        const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w}, cw[4] = {cv.x, cv.y, cv.z, cv.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            hp[4 * j + k] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, xw[k]) - __builtin_bit_cast(half2_t, cw[k]));
+    }
+    // byte planes of the magnitudes (sign bits dropped): hb = bits 14..8, lb = bits 7..0
+    uint32_t hb[8], lb[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        hp[i] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, xw[i]) - __builtin_bit_cast(half2_t, cw[i]));
-        mp[i] = hp[i] & 0x7FFF7FFFu;
+        const uint32_t m0 = hp[2 * i] & 0x7FFF7FFFu, m1 = hp[2 * i + 1] & 0x7FFF7FFFu;
+        hb[i] = __builtin_amdgcn_perm(m1, m0, 0x07050301u) | kByteTop;
+        lb[i] = __builtin_amdgcn_perm(m1, m0, 0x06040200u);
     }
-    // M = the largest magnitude with at least nnz of the token's magnitudes >= M
-    uint32_t m = 0;
-#pragma unroll 1
-    for (int bit = 14; bit >= 0; --bit) {
-        const uint32_t cand = m | (1u << bit);
-        const int ge = kDim - token_sum8(count_below(mp, cand));
-        m = ge >= nnz ? cand : m;
-    }
-    // channels above M, channels equal to M
-    uint32_t gt = 0, eq = 0;
+    // A: high byte H of M
+    const uint32_t h4 = search7(hb, 0, nnz);
+    uint32_t gt_h[8], eq_h[8], l7[8];
+    int above = 0;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        const uint32_t v = (mp[i >> 1] >> (16 * (i & 1))) & 0xFFFFu;
-        gt |= (v > m ? 1u : 0u) << i;
-        eq |= (v == m ? 1u : 0u) << i;
+    for (int i = 0; i < 8; ++i) {
+        gt_h[i] = ge_flags(hb[i], h4 + kByteOne);  // H + 1 <= 0x80: no carry between bytes
+        eq_h[i] = ge_flags(hb[i], h4) & ~gt_h[i];
+        above += __builtin_popcount(gt_h[i]);
+        // bits 7..1 of the low byte where the high byte is H, else 0 (bytes of eq_h - (eq_h >> 7) are 0x7F or 0)
+        l7[i] = ((lb[i] >> 1) & (eq_h[i] - (eq_h[i] >> 7))) | kByteTop;
     }
-    const int need = nnz - token_sum8(__builtin_popcount(gt));  // ties to take, lowest channels first
-    int quota = need - token_prefix8(__builtin_popcount(eq), tile);
+    above = quad_sum(above);
+    // B: bits 7..1 of M
+    const uint32_t l4 = search7(l7, above, nnz);
+    uint32_t gt_l[8], eq_l[8], one[8];
+    int above_l = 0, ones = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        gt_l[i] = ge_flags(l7[i], l4 + kByteOne);            // high byte H, bits 7..1 above L
+        eq_l[i] = ge_flags(l7[i], l4) & ~gt_l[i] & eq_h[i];  // high byte H, bits 7..1 equal to L
+        one[i] = eq_l[i] & (lb[i] << 7);                      // ... with bit 0 set
+        above_l += __builtin_popcount(gt_l[i]);
+        ones += __builtin_popcount(one[i]);
+    }
+    above += quad_sum(above_l);
+    ones = quad_sum(ones);
+    // C: bit 0 of M
+    const bool m_odd = above + ones >= nnz;
+    const int need = nnz - (m_odd ? above : above + ones);  // ties to take, lowest channels first
+    uint32_t gt[8], eq[8];
+    int n_eq = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        gt[i] = gt_h[i] | gt_l[i] | (m_odd ? 0u : one[i]);
+        eq[i] = m_odd ? one[i] : eq_l[i] & ~one[i];
+        n_eq += __builtin_popcount(eq[i]);
+    }
+    int quota = need - quad_prefix(n_eq, q);
     quota = quota < 0 ? 0 : quota;
-    while (__builtin_popcount(eq) > quota) eq &= ~(0x80000000u >> __builtin_clz(eq));  // drop the highest tie
-    const uint32_t sel = gt | eq;
-    // payload: the token's kept residuals in channel order
-    uint16_t* prow = payload + row * nnz + token_prefix8(__builtin_popcount(sel), tile);
+    while (n_eq > quota) {  // drop the highest-channel tie
+        int top = 0;
 #pragma unroll
-    for (int i = 0; i < 16; ++i)
-        if ((sel >> i) & 1u) prow[__builtin_popcount(sel & ((1u << i) - 1u))] = (uint16_t)(hp[i >> 1] >> (16 * (i & 1)));
-    // channel d -> bit (63 - d % 64) of word d / 64 (compression.py:87-88)
-    const uint32_t rev = __builtin_bitreverse32(sel) >> 16;  // channel 16 tile + i -> bit 15 - i
-    uint32_t lo = (tile & 1) ? rev : rev << 16, hi = lo;     // 32-bit halves of the tile pair
-    lo = (tile & 2) ? lo : 0u;
-    hi = (tile & 2) ? 0u : hi;
-    lo |= dpp_u<0xB1>(lo);
-    hi |= dpp_u<0xB1>(hi);
-    lo |= dpp_u<0x4E>(lo);
-    hi |= dpp_u<0x4E>(hi);
-    if ((tile & 3) == 0) meta[row * 2 + (tile >> 2)] = (int64_t)(((uint64_t)hi << 32) | lo);
+        for (int i = 1; i < 8; ++i) top = eq[i] ? i : top;
+        uint32_t w = eq[0];
+#pragma unroll
+        for (int i = 1; i < 8; ++i) w = i == top ? eq[i] : w;
+        const uint32_t cleared = w & ~(0x80000000u >> __builtin_clz(w));
+#pragma unroll
+        for (int i = 0; i < 8; ++i) eq[i] = i == top ? cleared : eq[i];
+        --n_eq;
+    }
+    // kept channels as a 32-bit mask, bit i = channel 32 q + i
+    uint32_t sel = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) sel |= movemask4(gt[i] | eq[i]) << (4 * i);
+    // the token keeps exactly nnz channels; the bound check keeps the LDS row
+    // writes inside the row regardless
+    const int kept = __builtin_popcount(sel);
+    const int first = quad_prefix(kept, q);
+    if (first + kept > nnz) sel = 0;
+    // channel d -> bit (63 - d % 64) of word d / 64 (compression.py:87-88):
+    // lane 2w holds the high half of word w, lane 2w + 1 the low half
+    const uint32_t rev = __builtin_bitreverse32(sel);
+    const uint32_t rev_next = dpp_u<0xB1>(rev);
+    if (valid && (q & 1) == 0) meta[row * 2 + (q >> 1)] = (int64_t)(((uint64_t)rev << 32) | rev_next);
+    // payload: kept residuals in channel order into the token's LDS row (others
+    // to the lane's dump slot), then the wave's rows to HBM
+    uint16_t* srow = s_rows[wave];
+    uint16_t* my_row = srow + (lane >> 2) * nnz;
+    uint16_t* dump = srow + kBitmapDump + lane;
+    int rank = first;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+        const int bit = (int)((sel >> i) & 1u);
+        uint16_t* dst = bit ? my_row + rank : dump;
+        *dst = (uint16_t)(hp[i >> 1] >> (16 * (i & 1)));
+        rank += bit;
+    }
+    wave_sync();
+    const int ntok = T - t_wave < kBitmapTokensPerWave ? T - t_wave : kBitmapTokensPerWave;
+    uint16_t* grow = payload + (bh * T + t_wave) * (long)nnz;  // the wave's rows are contiguous
+    const int halves = ntok * nnz;
+    if ((nnz & 7) == 0) {
+        const uint4* src = reinterpret_cast<const uint4*>(srow);
+        uint4* dst = reinterpret_cast<uint4*>(grow);
+        for (int c = lane; c < halves / 8; c += kWave) dst[c] = src[c];
+    } else {
+        for (int c = lane; c < halves; c += kWave) grow[c] = srow[c];
+    }
 }
 
 template <int BITS>
@@ -437,6 +549,39 @@ int check_common(const void* keys, const void* cent, const void* ids, int B, int
     return 0;
 }
 
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+// 4:16 fast path: nnz 32, 16-byte aligned tokens and centroids, 8-byte aligned payload.
+bool tile4_ok(const EncSides& S, int sides, int nnz) {
+    bool ok = nnz == 32;
+    for (int i = 0; i < sides; ++i)
+        ok = ok && aligned16(S.x[i]) && aligned16(S.cent[i]) && ((uintptr_t)S.payload[i] & 7u) == 0;
+    return ok;
+}
+int launch_tile4(const EncSides& S, int sides, int B, int H, int T, int struct_index, hipStream_t st) {
+    const long rows = (long)B * H * T;
+    hipLaunchKernelGGL(encode_tile4_kernel, dim3((int)((rows + 31) / 32), sides), dim3(256), 0, st, S, rows, T,
+                       struct_index);
+    return reskv_host::check_launch("encode_tile4_kernel");
+}
+
+// bitmap fast path: 16-byte aligned tokens, centroids and payload.
+bool bitmap4_ok(const EncSides& S, int sides) {
+    bool ok = true;
+    for (int i = 0; i < sides; ++i) ok = ok && aligned16(S.x[i]) && aligned16(S.cent[i]) && aligned16(S.payload[i]);
+    return ok;
+}
+int launch_bitmap4(const EncSides& S, int sides, int B, int H, int T, int nnz, hipStream_t st) {
+    const int BH = B * H;
+    const int per_block = kWavesPerBlock * kBitmapTokensPerWave;
+    for (int bh0 = 0; bh0 < BH; bh0 += 65535) {  // grid y covers at most 65535 (batch, head) rows
+        const dim3 grid((T + per_block - 1) / per_block, BH - bh0 < 65535 ? BH - bh0 : 65535, sides);
+        hipLaunchKernelGGL(encode_bitmap4_kernel, grid, dim3(256), 0, st, S, T, nnz, bh0);
+        if (reskv_host::check_launch("encode_bitmap4_kernel")) return 1;
+    }
+    return 0;
+}
+
 }  // namespace
 
 extern "C" int reskv_compress_fp16(const void* keys, const void* centroids, const int32_t* ids,
@@ -448,12 +593,9 @@ extern "C" int reskv_compress_fp16(const void* keys, const void* centroids, cons
                   "FP16 tile encoder requires nnz divisible by 8 and < 128");
     RESKV_REQUIRE(!struct_index || nnz == 32, "4:16 index codes require nnz == 32");
     const long rows = (long)B * H * T;
-    if (nnz == 32 && (((uintptr_t)keys | (uintptr_t)centroids) & 15u) == 0 && ((uintptr_t)payload & 7u) == 0) {
-        hipLaunchKernelGGL(encode_tile4_kernel, dim3((int)((rows + 31) / 32)), dim3(256), 0, (hipStream_t)stream,
-                           (const uint16_t*)keys, (const uint16_t*)centroids, ids, (uint16_t*)payload, meta, rows, T,
-                           C, struct_index);
-        return reskv_host::check_launch("encode_tile4_kernel");
-    }
+    const EncSides S{{(const uint16_t*)keys, nullptr}, {(const uint16_t*)centroids, nullptr}, {ids, nullptr},
+                     {(uint16_t*)payload, nullptr}, {meta, nullptr}, {C, 0}};
+    if (tile4_ok(S, 1, nnz)) return launch_tile4(S, 1, B, H, T, struct_index, (hipStream_t)stream);
     hipLaunchKernelGGL(encode_qtile_kernel, dim3(grid_for(rows)), dim3(256), 0, (hipStream_t)stream,
                        (const uint16_t*)keys, (const uint16_t*)centroids, ids, (uint16_t*)payload, meta,
                        rows, T, C, nnz, struct_index);
@@ -467,12 +609,9 @@ extern "C" int reskv_compress_bitmap(const void* keys, const void* centroids, co
     RESKV_REQUIRE(payload && meta, "null output pointer");
     RESKV_REQUIRE(nnz > 0 && nnz <= kDim, "nnz must be in [1, 128]");
     const long rows = (long)B * H * T;
-    if ((((uintptr_t)keys | (uintptr_t)centroids) & 15u) == 0) {
-        hipLaunchKernelGGL(encode_bitmap8_kernel, dim3((int)((rows + 31) / 32)), dim3(256), 0, (hipStream_t)stream,
-                           (const uint16_t*)keys, (const uint16_t*)centroids, ids, (uint16_t*)payload, meta, rows, T,
-                           C, nnz);
-        return reskv_host::check_launch("encode_bitmap8_kernel");
-    }
+    const EncSides S{{(const uint16_t*)keys, nullptr}, {(const uint16_t*)centroids, nullptr}, {ids, nullptr},
+                     {(uint16_t*)payload, nullptr}, {meta, nullptr}, {C, 0}};
+    if (bitmap4_ok(S, 1)) return launch_bitmap4(S, 1, B, H, T, nnz, (hipStream_t)stream);
     hipLaunchKernelGGL(encode_bitmap_kernel, dim3(grid_for(rows)), dim3(256), 0, (hipStream_t)stream,
                        (const uint16_t*)keys, (const uint16_t*)centroids, ids, (uint16_t*)payload, meta,
                        rows, T, C, nnz);
@@ -508,4 +647,38 @@ extern "C" int reskv_compress_structured_int4(const void* keys, const void* cent
                        (const uint16_t*)keys, (const uint16_t*)centroids, ids, qpacked, qmeta,
                        (uint16_t*)qscale, rows, T, C);
     return reskv_host::check_launch("encode_struct_int4_kernel");
+}
+
+// A layer's K and V in one launch (grid side dimension); each result equals
+// the single-tensor call's.  Inputs that miss the fast path's alignment run
+// as two single-tensor calls.
+extern "C" int reskv_compress_fp16_kv(const void* k, const void* v, const void* k_centroids,
+                                      const void* v_centroids, const int32_t* k_ids, const int32_t* v_ids,
+                                      void* k_payload, void* v_payload, int32_t* k_meta, int32_t* v_meta, int B,
+                                      int H, int T, int Ck, int Cv, int nnz, int struct_index, void* stream) {
+    if (check_common(k, k_centroids, k_ids, B, H, T, Ck) || check_common(v, v_centroids, v_ids, B, H, T, Cv))
+        return 1;
+    RESKV_REQUIRE(k_payload && v_payload && k_meta && v_meta, "null output pointer");
+    const EncSides S{{(const uint16_t*)k, (const uint16_t*)v}, {(const uint16_t*)k_centroids, (const uint16_t*)v_centroids},
+                     {k_ids, v_ids}, {(uint16_t*)k_payload, (uint16_t*)v_payload}, {k_meta, v_meta}, {Ck, Cv}};
+    if (tile4_ok(S, 2, nnz) && (!struct_index || nnz == 32))
+        return launch_tile4(S, 2, B, H, T, struct_index, (hipStream_t)stream);
+    if (reskv_compress_fp16(k, k_centroids, k_ids, k_payload, k_meta, B, H, T, Ck, nnz, struct_index, stream))
+        return 1;
+    return reskv_compress_fp16(v, v_centroids, v_ids, v_payload, v_meta, B, H, T, Cv, nnz, struct_index, stream);
+}
+
+extern "C" int reskv_compress_bitmap_kv(const void* k, const void* v, const void* k_centroids,
+                                        const void* v_centroids, const int32_t* k_ids, const int32_t* v_ids,
+                                        void* k_payload, void* v_payload, int64_t* k_meta, int64_t* v_meta, int B,
+                                        int H, int T, int Ck, int Cv, int nnz, void* stream) {
+    if (check_common(k, k_centroids, k_ids, B, H, T, Ck) || check_common(v, v_centroids, v_ids, B, H, T, Cv))
+        return 1;
+    RESKV_REQUIRE(k_payload && v_payload && k_meta && v_meta, "null output pointer");
+    RESKV_REQUIRE(nnz > 0 && nnz <= kDim, "nnz must be in [1, 128]");
+    const EncSides S{{(const uint16_t*)k, (const uint16_t*)v}, {(const uint16_t*)k_centroids, (const uint16_t*)v_centroids},
+                     {k_ids, v_ids}, {(uint16_t*)k_payload, (uint16_t*)v_payload}, {k_meta, v_meta}, {Ck, Cv}};
+    if (bitmap4_ok(S, 2)) return launch_bitmap4(S, 2, B, H, T, nnz, (hipStream_t)stream);
+    if (reskv_compress_bitmap(k, k_centroids, k_ids, k_payload, k_meta, B, H, T, Ck, nnz, stream)) return 1;
+    return reskv_compress_bitmap(v, v_centroids, v_ids, v_payload, v_meta, B, H, T, Cv, nnz, stream);
 }

@@ -20,7 +20,8 @@ def declared_functions():
 def test_header_declares_the_operator_surface():
     names = declared_functions()
     for required in ("reskv_compress_fp16", "reskv_compress_bitmap", "reskv_compress_quantized",
-                     "reskv_compress_structured_int4", "reskv_kmeans", "reskv_kmeans_assign", "reskv_kmeans_kv",
+                     "reskv_compress_structured_int4", "reskv_compress_fp16_kv", "reskv_compress_bitmap_kv",
+                     "reskv_kmeans", "reskv_kmeans_assign", "reskv_kmeans_kv",
                      "reskv_decode",
                      "reskv_merge_recent_scores", "reskv_merge_recent_qk", "reskv_decode_recent",
                      "reskv_decode_dense"):
@@ -32,13 +33,13 @@ def test_library_exports_every_declared_symbol():
     for name in declared_functions():
         assert hasattr(lib, name), name
         assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
-    assert lib.reskv_abi_version() == _lib.ABI_VERSION == 3
+    assert lib.reskv_abi_version() == _lib.ABI_VERSION == 4
 
 
 def test_a_library_of_another_abi_version_is_refused(monkeypatch):
     monkeypatch.setattr(_lib, "_lib", None)
-    monkeypatch.setattr(_lib, "ABI_VERSION", 2)
-    with pytest.raises(RuntimeError, match="ABI version 3, this binding needs 2"):
+    monkeypatch.setattr(_lib, "ABI_VERSION", 3)
+    with pytest.raises(RuntimeError, match="ABI version 4, this binding needs 3"):
         _lib.lib()
     assert _lib._lib is None  # nothing half-loaded is kept
 

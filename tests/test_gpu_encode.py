@@ -96,6 +96,24 @@ def test_encoders_at_config1_scale_round_trip(ext, device):
     assert np.array_equal(np_(m), em) and np.array_equal(np_(p).view(np.uint16), ep.view(np.uint16))
 
 
+@pytest.mark.parametrize("t", [77, 300])
+@pytest.mark.parametrize("fmt,nnz,struct", [("bitmap", 64, None), ("bitmap", 32, None), ("bitmap", 24, None),
+                                            ("tile", 32, True), ("tile", 32, False), ("tile", 64, False)])
+def test_kv_encoders_equal_single_tensor_calls(ext, device, t, fmt, nnz, struct):
+    """K and V in one launch (different data, 5 and 3 centroids) give exactly the two single calls' results."""
+    k, kc, ki = _case("normal", 2, 3, t, 5, 3, device)
+    v, vc, vi = _case("ties", 2, 3, t, 3, 4, device)
+    if fmt == "bitmap":
+        pair = ext.compress_bitmap_kv(k, kc, ki, v, vc, vi, nnz)
+        single = (ext.compress_bitmap(k, kc, ki, nnz), ext.compress_bitmap(v, vc, vi, nnz))
+    else:
+        pair = ext.compress_fp16_kv(k, kc, ki, v, vc, vi, nnz, struct)
+        single = (ext.compress_fp16(k, kc, ki, nnz, struct), ext.compress_fp16(v, vc, vi, nnz, struct))
+    for got, want in zip(pair, single):
+        for a, b in zip(got, want):
+            assert torch.equal(a, b)
+
+
 def test_encoder_rejects_bad_inputs(ext, device):
     x = torch.zeros(1, 1, 4, 128, dtype=torch.float16, device=device)
     c = torch.zeros(1, 1, 2, 128, dtype=torch.float16, device=device)
@@ -106,3 +124,5 @@ def test_encoder_rejects_bad_inputs(ext, device):
         ext.compress_fp16(x, c, ids, 64, True)
     with pytest.raises(RuntimeError, match="float16"):
         ext.compress_bitmap(x.float(), c, ids, 32)
+    with pytest.raises(RuntimeError, match="identical shapes"):
+        ext.compress_bitmap_kv(x, c, ids, x[:, :, :2].contiguous(), c, ids[:, :, :2].contiguous(), 32)
