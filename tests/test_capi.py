@@ -55,6 +55,8 @@ def test_null_pointers_are_rejected_without_a_gpu():
     assert "null" in _err(lib.reskv_compress_bitmap(None, None, None, None, None, 1, 1, 1, 1, 32, None))
     assert "null" in _err(lib.reskv_kmeans(None, None, None, None, 1, 1, 1, 1, 0, None, 0, None))
     assert "null" in _err(lib.reskv_kmeans_kv(*([None] * 8), 1, 1, 1, 1, None, 0, None))
+    assert "null" in _err(lib.reskv_compress_fp16_kv(*([None] * 10), 1, 1, 1, 4, 4, 32, 1, None))
+    assert "null" in _err(lib.reskv_compress_bitmap_kv(*([None] * 10), 1, 1, 1, 4, 4, 32, None))
     assert "null" in _err(lib.reskv_merge_recent_qk(None, None, None, None, None, None, 1, 4, 1, 1, 0, 1.0, None,
                                                     None))
     assert "null" in _err(lib.reskv_decode_recent(None, None, None, None, None, 1, 4, 1, 16, 0, 15, 1.0, 0, None,
@@ -78,6 +80,15 @@ def test_encoder_argument_checks(args, message):
     st = lib.reskv_compress_fp16(p, p, p, p, p, kw["B"], kw["H"], kw["T"], kw["C"], kw["nnz"],
                                  kw["struct_index"], None)
     assert message in _err(st)
+
+
+def test_kv_encoder_argument_checks():
+    lib = _lib.lib()
+    p = ctypes.c_void_p(16)  # never dereferenced: validation fails first
+    assert "centroid count" in _err(lib.reskv_compress_bitmap_kv(*([p] * 10), 1, 1, 4, 4, 65, 32, None))
+    assert "nnz" in _err(lib.reskv_compress_bitmap_kv(*([p] * 10), 1, 1, 4, 4, 4, 0, None))
+    assert "positive" in _err(lib.reskv_compress_fp16_kv(*([p] * 10), 1, 0, 4, 4, 4, 32, 1, None))
+    assert "divisible by 8" in _err(lib.reskv_compress_fp16_kv(*([p] * 10), 1, 1, 4, 4, 4, 30, 0, None))
 
 
 def test_quantiser_argument_checks():
