@@ -88,10 +88,16 @@ int reskv_compress_structured_int4(const void* keys, const void* centroids,
 /* Bytes of scratch reskv_kmeans needs for these sizes. */
 int64_t reskv_kmeans_workspace_bytes(int BH, int T, int C);
 
-/* Lloyd iterations with centres initialised by the caller.
+/* torch.linspace(0, T-1, C).long() as torch evaluates it in fp32 (the
+ * initial-centre rows of reskv/compression.py:35); rows int32 [C], host
+ * memory.  Needs 1 <= C <= 64 and T >= C. */
+int reskv_linspace_rows(int T, int C, int32_t* rows);
+
+/* Lloyd iterations from given initial centres.
  * Replaces the torch loop of reskv/compression.py:37-53 (cdist, argmin,
- * one_hot, bmm).  x fp16 [BH,T,128]; centers_init fp32 [BH,C,128] (the
- * linspace-selected tokens); centers_out fp16 [BH,C,128]; ids int32 [BH,T]
+ * one_hot, bmm).  x fp16 [BH,T,128]; centers_init fp32 [BH,C,128], or null:
+ * the tokens at reskv_linspace_rows(T, C) of each problem (compression.py:
+ * 34-36; T >= C), gathered on the device; centers_out fp16 [BH,C,128]; ids int32 [BH,T]
  * (from the last assignment).  value_mode=0: K semantics (fp32 distances,
  * empty cluster keeps its centre); 1: V semantics (the fp16 cdist of
  * compression.py:38 -- fp16 norms, fp16 distance, fp16 root, lowest index on
@@ -103,7 +109,8 @@ int reskv_kmeans(const void* x, const float* centers_init, void* centers_out, in
 /* A layer's K and V clustered together: the two Lloyd runs of
  * reskv/compression.py:164-165 (cluster(key), cluster(value, value=True)) as
  * one sequence of launches over 2*BH problems, K rules for k and V rules for v.
- * k, v fp16 [BH,T,128]; init_k, init_v fp32 [BH,C,128]; out_k, out_v fp16
+ * k, v fp16 [BH,T,128]; init_k, init_v fp32 [BH,C,128] (both null: the
+ * linspace tokens, as in reskv_kmeans); out_k, out_v fp16
  * [BH,C,128]; ids_k, ids_v int32 [BH,T].  Each result equals the separate
  * reskv_kmeans call's.  workspace: reskv_kmeans_workspace_bytes(2*BH, T, C). */
 int reskv_kmeans_kv(const void* k, const void* v, const float* init_k, const float* init_v, void* out_k,

@@ -15,6 +15,7 @@ the input's device, and enqueues the kernels on torch's current stream of
 that device without synchronising.
 """
 
+import ctypes
 from functools import lru_cache
 from types import SimpleNamespace
 
@@ -243,49 +244,69 @@ def compress_structured_int4(keys, centroids, cluster_ids):
     return [qpacked, qmeta, qscale]
 
 
-def kmeans(x, centers_init, iterations, value):
-    """Lloyd k-means (reskv/compression.py:37-53) from caller-chosen initial centres.
+def _init_count(inits, count, t):
+    """The centroid count: from the given initial centres, or ``count`` for the
+    linspace tokens (reskv/compression.py:34-36), which need T >= count."""
+    given = [c for c in inits if c is not None]
+    _require(len(given) in (0, len(inits)), "give every initial centre array or none")
+    for c in given:
+        _require(c.dtype == torch.float32 and c.dim() == 3, "centres must be fp32 [BH,C,128]")
+    if given:
+        return given[0].shape[1]
+    _require(count is not None and 1 <= int(count) <= t, "linspace initial centres need 1 <= count <= T")
+    return int(count)
 
-    x fp16 [BH, T, 128]; centers_init fp32 [BH, C, 128].
+
+def linspace_rows(t, count):
+    """Initial-centre token rows, torch.linspace(0, T-1, count).long() evaluated in fp32 (host list)."""
+    rows = (ctypes.c_int32 * int(count))()
+    _lib.check(_lib.lib().reskv_linspace_rows(int(t), int(count), rows), "linspace_rows")
+    return list(rows)
+
+
+def kmeans(x, centers_init, iterations, value, count=None):
+    """Lloyd k-means (reskv/compression.py:37-53).
+
+    x fp16 [BH, T, 128]; centers_init fp32 [BH, C, 128], or None for the
+    tokens at linspace(0, T-1, count) of each row (gathered on the device).
     Returns (centres fp16 [BH, C, 128], ids int32 [BH, T]).
     """
     _require(x.dtype == torch.float16 and x.dim() == 3 and x.shape[2] == 128, "x must be fp16 [BH,T,128]")
-    _require(centers_init.dtype == torch.float32 and centers_init.dim() == 3, "centres must be fp32 [BH,C,128]")
-    dev = _dev_check(x, centers_init)
     bh, t, _ = x.shape
-    c = centers_init.shape[1]
+    c = _init_count((centers_init,), count, t)
+    dev = _dev_check(x, *(() if centers_init is None else (centers_init,)))
     out = _empty((bh, c, 128), torch.float16, dev)
     ids = _empty((bh, t), torch.int32, dev)
     L = _lib.lib()
     ws = _workspace(L.reskv_kmeans_workspace_bytes(bh, t, c), dev)
     with torch.cuda.device(dev):
-        _lib.check(L.reskv_kmeans(x.data_ptr(), centers_init.data_ptr(), out.data_ptr(), ids.data_ptr(), bh, t, c,
+        _lib.check(L.reskv_kmeans(x.data_ptr(), _ptr(centers_init), out.data_ptr(), ids.data_ptr(), bh, t, c,
                                   int(iterations), int(bool(value)), ws.data_ptr(), ws.numel(), _stream(dev)),
                    "kmeans")
     return out, ids
 
 
-def kmeans_kv(k, v, init_k, init_v, iterations):
+def kmeans_kv(k, v, init_k, init_v, iterations, count=None):
     """A layer's K and V clustered in one launch sequence (reskv/compression.py:164-165).
 
-    k, v fp16 [BH, T, 128]; init_k, init_v fp32 [BH, C, 128].  Returns
-    ((centres_k, ids_k), (centres_v, ids_v)), each equal to ``kmeans`` with
-    value=False for K and value=True for V.
+    k, v fp16 [BH, T, 128]; init_k, init_v fp32 [BH, C, 128], or both None for
+    the linspace tokens (``count`` of them).  Returns ((centres_k, ids_k),
+    (centres_v, ids_v)), each equal to ``kmeans`` with value=False for K and
+    value=True for V.
     """
-    for x, c in ((k, init_k), (v, init_v)):
+    for x in (k, v):
         _require(x.dtype == torch.float16 and x.dim() == 3 and x.shape[2] == 128, "x must be fp16 [BH,T,128]")
-        _require(c.dtype == torch.float32 and c.dim() == 3, "centres must be fp32 [BH,C,128]")
-    _require(k.shape == v.shape and init_k.shape == init_v.shape and init_k.shape[0] == k.shape[0],
-             "K and V must share [BH, T] and the centroid count")
-    dev = _dev_check(k, v, init_k, init_v)
     bh, t, _ = k.shape
-    c = init_k.shape[1]
+    c = _init_count((init_k, init_v), count, t)
+    _require(k.shape == v.shape and (init_k is None or (init_k.shape == init_v.shape and init_k.shape[0] == bh)),
+             "K and V must share [BH, T] and the centroid count")
+    dev = _dev_check(k, v, *(() if init_k is None else (init_k, init_v)))
     outs = [_empty((bh, c, 128), torch.float16, dev) for _ in range(2)]
     ids = [_empty((bh, t), torch.int32, dev) for _ in range(2)]
     L = _lib.lib()
     ws = _workspace(L.reskv_kmeans_workspace_bytes(2 * bh, t, c), dev)
     with torch.cuda.device(dev):
-        _lib.check(L.reskv_kmeans_kv(k.data_ptr(), v.data_ptr(), init_k.data_ptr(), init_v.data_ptr(),
+        _lib.check(L.reskv_kmeans_kv(k.data_ptr(), v.data_ptr(), _ptr(init_k), _ptr(init_v),
                                      outs[0].data_ptr(), outs[1].data_ptr(), ids[0].data_ptr(), ids[1].data_ptr(),
                                      bh, t, c, int(iterations), ws.data_ptr(), ws.numel(), _stream(dev)), "kmeans_kv")
     return (outs[0], ids[0]), (outs[1], ids[1])

@@ -44,6 +44,7 @@ SIGNATURES = {
     "reskv_compress_fp16": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp]),
     "reskv_compress_bitmap": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp]),
     "reskv_compress_fp16_kv": (_i, [_vp] * 10 + [_i] * 7 + [_vp]),
+    "reskv_linspace_rows": (_i, [_i, _i, _vp]),
     "reskv_compress_bitmap_kv": (_i, [_vp] * 10 + [_i] * 6 + [_vp]),
     "reskv_compress_quantized": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp]),
     "reskv_compress_structured_int4": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),

@@ -33,14 +33,12 @@ def _ops(x: torch.Tensor):
 
 
 def _initial_centers(data: torch.Tensor, count: int) -> torch.Tensor:
-    """Initial centres [BH, C, 128] fp32 (reskv/compression.py:28-36).
-
-    T >= C: the tokens at ``linspace(0, T-1, C).long()``; T < C: every token plus
-    C - T jittered copies of random tokens (not deterministic, as in the reference).
-    """
+    """Initial centres [BH, C, 128] fp32 when T < C (reskv/compression.py:28-33):
+    every token plus C - T jittered copies of random tokens (not deterministic,
+    as in the reference).  For T >= C the library takes the tokens at
+    ``linspace(0, T-1, C).long()`` itself (``reskv_linspace_rows``,
+    reskv/compression.py:34-36)."""
     t = data.shape[1]
-    if t >= count:
-        return data[:, torch.linspace(0, t - 1, count, device=data.device).long()].float().contiguous()
     pick = data[:, torch.randint(t, (count - t,), device=data.device)]
     return torch.cat((data, pick + torch.randn_like(pick) * 0.01), dim=1).float().contiguous()
 
@@ -56,10 +54,12 @@ def cluster(x: torch.Tensor, count: int = 32, iterations: int = 10, *, value: bo
     if value:
         count = min(count, t)
     rows = x.reshape(b * h, t, d).contiguous()
-    init = _initial_centers(rows, count)
-    if value:
-        init = init.half().float()  # V centres live in fp16 (reskv/compression.py:27)
-    centers, ids = _ops(x).kmeans(rows, init, iterations, value)
+    init = None  # T >= C: the library gathers the linspace tokens itself
+    if t < count:
+        init = _initial_centers(rows, count)
+        if value:
+            init = init.half().float()  # V centres live in fp16 (reskv/compression.py:27)
+    centers, ids = _ops(x).kmeans(rows, init, iterations, value, count)
     return centers.view(b, h, count, d), ids.view(b, h, t)
 
 
@@ -75,8 +75,8 @@ def cluster_kv(key: torch.Tensor, value: torch.Tensor, count: int = 32, iteratio
         return cluster(key, count, iterations), cluster(value, count, iterations, value=True)
     krows = key.reshape(b * h, t, d).contiguous()
     vrows = value.reshape(b * h, t, d).contiguous()
-    starts = (_initial_centers(krows, count), _initial_centers(vrows, count).half().float())
-    (kc, ki), (vc, vi) = _ops(key).kmeans_kv(krows, vrows, *starts, iterations)
+    # the linspace tokens of both tensors, gathered by the library (T >= C here)
+    (kc, ki), (vc, vi) = _ops(key).kmeans_kv(krows, vrows, None, None, iterations, count)
     shape_c, shape_i = (b, h, count, d), (b, h, t)
     return (kc.view(shape_c), ki.view(shape_i)), (vc.view(shape_c), vi.view(shape_i))
 

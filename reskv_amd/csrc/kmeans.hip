@@ -131,6 +131,32 @@ __global__ void __launch_bounds__(kDim) kmeans_prep_kernel(const float* __restri
     store_tables(v, true, pad, bh >= vfrom, c, thi + head, tlo + head, tnorm + bh * Cp + c, s_w);
 }
 
+// Row indices of the initial centres (at most kMaxClusters), passed by value.
+struct InitRows {
+    int idx[kMaxClusters];
+};
+
+// As kmeans_prep_kernel, with the initial centre c of problem bh taken from
+// token idx[c] of that problem's rows (fp16, exact in fp32), also written to
+// the fp32 centre array.
+__global__ void __launch_bounds__(kDim) kmeans_prep_rows_kernel(Problems P, InitRows ir, float* __restrict__ centers,
+                                                                uint16_t* __restrict__ thi, uint16_t* __restrict__ tlo,
+                                                                float* __restrict__ tnorm, int T, int C, int Cp) {
+    __shared__ float s_w[2];
+    const int c = blockIdx.x;
+    const long bh = blockIdx.y;
+    const bool pad = c >= C;
+    const int side = side_of(P, bh);
+    const long pb = bh - (side ? P.split : 0);
+    float v = 0.0f;
+    if (!pad) {
+        v = h2f(P.x[side][(pb * T + ir.idx[c]) * kDim + threadIdx.x]);
+        centers[(bh * C + c) * kDim + threadIdx.x] = v;
+    }
+    const long head = bh * Cp * kDim;
+    store_tables(v, true, pad, bh >= P.vfrom, c, thi + head, tlo + head, tnorm + bh * Cp + c, s_w);
+}
+
 // |c|^2 of centre r of a lane's four
 __device__ __forceinline__ float cnorm(float4 n, int r) { return r == 0 ? n.x : r == 1 ? n.y : r == 2 ? n.z : n.w; }
 
@@ -587,8 +613,26 @@ int check_pointers(const void* x, const void* workspace) {
     return 0;
 }
 
+// torch.linspace(0, T - 1, C).long() (reskv/compression.py:35) as torch
+// evaluates it in fp32: step = fl32((T - 1) / (C - 1)); index i < C / 2 is
+// fl32(i * step), the others fl32((T - 1) - (C - 1 - i) * step) (one rounding
+// of the exact value, as torch's fused form), truncated toward zero.
+void linspace_rows(int T, int C, int* idx) {
+    if (C == 1) {
+        idx[0] = 0;
+        return;
+    }
+    const float end = (float)(T - 1);
+    const float step = end / (float)(C - 1);
+    for (int i = 0; i < C; ++i) {
+        const float v = i < C / 2 ? (float)i * step : fmaf(-(float)(C - 1 - i), step, end);
+        idx[i] = (int)v;
+    }
+}
+
 // Lloyd iterations over BH problems; init[side] holds the initial fp32
-// centres of the problems in tensor `side`.
+// centres of the problems in tensor `side`, or both are null: the tokens at
+// linspace(0, T - 1, C) of each problem (T >= C).
 int run_kmeans(const Problems& P, const float* const init[2], int BH, int T, int C, int iterations, void* workspace,
                hipStream_t st) {
     const Layout L = layout(BH, T, C);
@@ -597,14 +641,22 @@ int run_kmeans(const Problems& P, const float* const init[2], int BH, int T, int
     float* centers = (float*)(w + L.centers);
     float* psum = (float*)(w + L.psum);
     int* pcnt = (int*)(w + L.pcnt);
-    const size_t row = (size_t)C * kDim * sizeof(float);
-    for (int side = 0; side < 2; ++side) {
-        const int n = side ? BH - P.split : P.split;
-        if (n > 0 && hipMemcpyAsync(centers + (side ? (size_t)P.split * C * kDim : 0), init[side], n * row,
-                                    hipMemcpyDeviceToDevice, st) != hipSuccess)
-            return reskv_host::check_launch("kmeans centre copy");
+    if (init[0] == nullptr && init[1] == nullptr) {
+        InitRows ir{};
+        linspace_rows(T, C, ir.idx);
+        hipLaunchKernelGGL(kmeans_prep_rows_kernel, dim3(L.Cp, BH), dim3(kDim), 0, st, P, ir, centers, tb.hi, tb.lo,
+                           tb.norm, T, C, L.Cp);
+        if (reskv_host::check_launch("kmeans_prep_rows_kernel")) return 1;
+    } else {
+        const size_t row = (size_t)C * kDim * sizeof(float);
+        for (int side = 0; side < 2; ++side) {
+            const int n = side ? BH - P.split : P.split;
+            if (n > 0 && hipMemcpyAsync(centers + (side ? (size_t)P.split * C * kDim : 0), init[side], n * row,
+                                        hipMemcpyDeviceToDevice, st) != hipSuccess)
+                return reskv_host::check_launch("kmeans centre copy");
+        }
+        if (launch_prep(centers, tb, BH, C, L.Cp, P.vfrom, st)) return 1;
     }
-    if (launch_prep(centers, tb, BH, C, L.Cp, P.vfrom, st)) return 1;
     for (int it = 0; it < iterations; ++it) {
         if (launch_assign(P, tb, psum, pcnt, BH, T, C, L, st)) return 1;
         const bool last = it == iterations - 1;
@@ -640,10 +692,20 @@ extern "C" int reskv_kmeans_assign(const void* x, const float* centers, int32_t*
     return launch_assign(P, tb, nullptr, nullptr, BH, T, C, L, st);
 }
 
+extern "C" int reskv_linspace_rows(int T, int C, int32_t* rows) {
+    RESKV_REQUIRE(rows != nullptr, "null pointer argument");
+    RESKV_REQUIRE(C >= 1 && C <= kMaxClusters && T >= C, "need 1 <= C <= 64 and T >= C");
+    int idx[kMaxClusters];
+    linspace_rows(T, C, idx);
+    for (int i = 0; i < C; ++i) rows[i] = idx[i];
+    return 0;
+}
+
 extern "C" int reskv_kmeans(const void* x, const float* centers_init, void* centers_out, int32_t* ids,
                             int BH, int T, int C, int iterations, int value_mode, void* workspace,
                             int64_t workspace_bytes, void* stream) {
-    RESKV_REQUIRE(x && centers_init && centers_out && ids, "null pointer argument");
+    RESKV_REQUIRE(x && centers_out && ids, "null pointer argument");
+    RESKV_REQUIRE(centers_init || T >= C, "linspace initial centres need T >= C");
     RESKV_REQUIRE(BH > 0 && T > 0, "problem sizes must be positive");
     RESKV_REQUIRE(C >= 1 && C <= kMaxClusters, "centroid count must be in [1, 64]");
     RESKV_REQUIRE(iterations >= 1, "iterations must be positive");
@@ -660,7 +722,9 @@ extern "C" int reskv_kmeans(const void* x, const float* centers_init, void* cent
 extern "C" int reskv_kmeans_kv(const void* k, const void* v, const float* init_k, const float* init_v, void* out_k,
                                void* out_v, int32_t* ids_k, int32_t* ids_v, int BH, int T, int C, int iterations,
                                void* workspace, int64_t workspace_bytes, void* stream) {
-    RESKV_REQUIRE(k && v && init_k && init_v && out_k && out_v && ids_k && ids_v, "null pointer argument");
+    RESKV_REQUIRE(k && v && out_k && out_v && ids_k && ids_v, "null pointer argument");
+    RESKV_REQUIRE((init_k == nullptr) == (init_v == nullptr), "give both initial centre arrays or neither");
+    RESKV_REQUIRE(init_k || T >= C, "linspace initial centres need T >= C");
     RESKV_REQUIRE(BH > 0 && T > 0, "problem sizes must be positive");
     RESKV_REQUIRE(C >= 1 && C <= kMaxClusters, "centroid count must be in [1, 64]");
     RESKV_REQUIRE(iterations >= 1, "iterations must be positive");

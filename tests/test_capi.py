@@ -54,6 +54,9 @@ def test_null_pointers_are_rejected_without_a_gpu():
     assert "null" in _err(lib.reskv_compress_fp16(None, None, None, None, None, 1, 1, 1, 1, 32, 1, None))
     assert "null" in _err(lib.reskv_compress_bitmap(None, None, None, None, None, 1, 1, 1, 1, 32, None))
     assert "null" in _err(lib.reskv_kmeans(None, None, None, None, 1, 1, 1, 1, 0, None, 0, None))
+    p = ctypes.c_void_p(16)
+    assert "both initial centre arrays or neither" in _err(lib.reskv_kmeans_kv(p, p, p, None, p, p, p, p, 1, 4, 2, 1,
+                                                                                p, 1 << 20, None))
     assert "null" in _err(lib.reskv_kmeans_kv(*([None] * 8), 1, 1, 1, 1, None, 0, None))
     assert "null" in _err(lib.reskv_compress_fp16_kv(*([None] * 10), 1, 1, 1, 4, 4, 32, 1, None))
     assert "null" in _err(lib.reskv_compress_bitmap_kv(*([None] * 10), 1, 1, 1, 4, 4, 32, None))
@@ -89,6 +92,30 @@ def test_kv_encoder_argument_checks():
     assert "nnz" in _err(lib.reskv_compress_bitmap_kv(*([p] * 10), 1, 1, 4, 4, 4, 0, None))
     assert "positive" in _err(lib.reskv_compress_fp16_kv(*([p] * 10), 1, 0, 4, 4, 4, 32, 1, None))
     assert "divisible by 8" in _err(lib.reskv_compress_fp16_kv(*([p] * 10), 1, 1, 4, 4, 4, 30, 0, None))
+
+
+def test_linspace_rows_match_torch_and_the_oracle():
+    """The library's initial-centre rows equal torch.linspace(0, T-1, C).long()
+    (reskv/compression.py:35) and the oracle's restatement."""
+    import numpy as np
+    import torch
+
+    from oracle import reskv_oracle as o
+
+    lib = _lib.lib()
+    for t in (1, 2, 3, 33, 64, 65, 100, 960, 1000, 4095, 8156, 8192, 16384, 65536, 1 << 20):
+        for c in (1, 2, 7, 31, 32, 33, 63, 64):
+            if t < c:
+                continue
+            rows = (ctypes.c_int32 * c)()
+            assert lib.reskv_linspace_rows(t, c, rows) == 0
+            got = np.array(list(rows))
+            assert np.array_equal(got, torch.linspace(0, t - 1, c).long().numpy()), (t, c)
+            assert np.array_equal(got, o.linspace_indices(t, c)), (t, c)
+    rows = (ctypes.c_int32 * 4)()
+    assert "T >= C" in _err(lib.reskv_linspace_rows(3, 4, rows))
+    assert "T >= C" in _err(lib.reskv_kmeans(ctypes.c_void_p(16), None, ctypes.c_void_p(16), ctypes.c_void_p(16),
+                                              1, 3, 4, 1, 0, ctypes.c_void_p(256), 1 << 20, None))
 
 
 def test_quantiser_argument_checks():

@@ -203,3 +203,25 @@ def test_paired_kv_clustering_at_config1_scale(device):
     ev, evi = cluster(v, 32, 3, value=True)
     assert torch.equal(ki, eki) and torch.equal(vi, evi)
     assert torch.equal(kc, ek) and torch.equal(vc, ev)
+
+
+@pytest.mark.parametrize("t,count", [(8156, 32), (333, 64), (64, 64), (17, 1)])
+def test_library_linspace_init_equals_explicit_centres(device, t, count):
+    """Initial centres gathered by the library (reskv_linspace_rows on the
+    device) give exactly the run from the same tokens passed as fp32 centres,
+    for K, V and the paired sequence."""
+    from reskv_amd._extension import load_extension
+
+    ops = load_extension("compression")
+    k, v, _ = outlier_kv(1, 4, t, seed=53)
+    rows_k, rows_v = (x.reshape(4, t, 128).contiguous() for x in (k, v))
+    idx = torch.from_numpy(o.linspace_indices(t, count)).to(device)
+    init_k, init_v = rows_k[:, idx].float(), rows_v[:, idx].float()
+    for rows, init, value in ((rows_k, init_k, False), (rows_v, init_v, True)):
+        got = ops.kmeans(rows, None, 3, value, count)
+        want = ops.kmeans(rows, init, 3, value)
+        assert torch.equal(got[0], want[0]) and torch.equal(got[1], want[1])
+    got = ops.kmeans_kv(rows_k, rows_v, None, None, 3, count)
+    want = ops.kmeans_kv(rows_k, rows_v, init_k, init_v, 3)
+    for g, w in zip(got, want):
+        assert torch.equal(g[0], w[0]) and torch.equal(g[1], w[1])
