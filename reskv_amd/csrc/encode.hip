@@ -285,11 +285,19 @@ __device__ __forceinline__ int quad_prefix(int v, int q) {
 }
 // Bit-7 flags of the bytes of p (each ORed with 0x80 beforehand) that are >= the bytes of c4.
 __device__ __forceinline__ uint32_t ge_flags(uint32_t p, uint32_t c4) { return (p - c4) & kByteTop; }
+// popcount(x) + acc as one v_bcnt_u32_b32 (the accumulate is the
+// instruction's own operand): written out so that a count over several words
+// stays a chain of these instead of being rebalanced into separate adds.
+__device__ __forceinline__ int bcnt_acc(uint32_t x, int acc) {
+    int r;
+    asm("v_bcnt_u32_b32 %0, %1, %2" : "=v"(r) : "v"(x), "v"(acc));
+    return r;
+}
 // Number of the lane's 32 plane bytes >= the bytes of c4.
 __device__ __forceinline__ int count_ge(const uint32_t* p, uint32_t c4) {
     int n = 0;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) n += __builtin_popcount(ge_flags(p[i], c4));
+    for (int i = 0; i < 8; ++i) n = bcnt_acc(ge_flags(p[i], c4), n);
     return n;
 }
 // Largest 7-bit c (as four equal bytes) with base + (token count of plane bytes >= c) >= nnz.
