@@ -461,6 +461,26 @@ def cpu_baseline():
             "configs": out}
 
 
+def copy_bandwidth(torch, device, nbytes=1 << 30, reps=10):
+    """GB/s of a plain device-to-device copy (bytes read + bytes written per
+    second): the bandwidth a streaming kernel reaches on this box, reported
+    beside the 8 TB/s spec-sheet peak."""
+    src = torch.empty(nbytes, dtype=torch.uint8, device=device).fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(2):
+        dst.copy_(src)
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    end.record()
+    end.synchronize()
+    secs = start.elapsed_time(end) / 1e3
+    del src, dst
+    torch.cuda.empty_cache()
+    return 2.0 * nbytes * reps / secs / 1e9
+
+
 def measured_traffic(b, t, sparsity, layout):
     """HBM bytes per launch of the partial kernel from the committed rocprof run, if it is this workload.
 
@@ -539,6 +559,7 @@ def main():
     if not args.no_e2e:
         e2e = measure_e2e(torch, device, args.e2e_batch, args.e2e_prompt, args.e2e_steps)
         print(json.dumps({"e2e": e2e}), flush=True)
+    copy_gbps = copy_bandwidth(torch, device)
     cpu = None if args.no_cpu_baseline else cpu_baseline()
     traffic = measured_traffic(args.batch, args.seq_len, args.sparsity, r["layout"])
     secs = r["seconds"]
@@ -581,6 +602,7 @@ def main():
             "frac": r["frac"], "traffic": traffic,
             "kernel": "one decode-attention call (decode_partial_kernel + decode_merge_kernel)",
             "bytes_per_call": r["bytes_per_call"],
+            "copy_GBps": copy_gbps, "frac_of_copy": r["achieved_GBps"] / copy_gbps,
         },
         "cpu_baseline": cpu,
     }
