@@ -46,7 +46,7 @@ def parse():
     p.add_argument("--no-sweep", action="store_true")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-e2e", action="store_true", help="leave the config-4 end-to-end decode out of the line")
-    p.add_argument("--e2e-steps", type=int, default=256,
+    p.add_argument("--e2e-steps", type=int, default=2048,
                    help="new tokens per sequence timed in the config-4 decode (config 4 names 2048)")
     p.add_argument("--e2e-batch", type=int, default=16)
     p.add_argument("--e2e-prompt", type=int, default=8192)
@@ -317,8 +317,9 @@ def measure_e2e(torch, device, batch=16, prompt=8192, steps=2048, warmup=4, attn
     torch.cuda.synchronize()
     out = {"prefill_s_incl_compression": time.perf_counter() - t0, "batch": batch, "prompt": prompt,
            "new_tokens_timed": steps, "config4_new_tokens": 2048,
-           "note": f"decode rates timed over {steps} greedy tokens after {warmup} warm-up tokens "
-                   f"(config 4 names 2048; the per-token work is the same, the history {prompt}+{steps})",
+           "note": (f"decode rates timed over {steps} greedy tokens after {warmup} warm-up tokens"
+                    + ("" if steps == 2048 else f" (config 4 names 2048; the per-token work is the same, "
+                                                 f"the history {prompt}+{steps})")),
            "model": "random-init Llama-3.1-8B shape (fp16 weights)"}
     for name, dec in decs.items():
         dec.start(first)
