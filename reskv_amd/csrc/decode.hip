@@ -45,6 +45,7 @@ constexpr int kVPitch = kDim + 8;  // halves per token row of the V transpose ti
 constexpr int kCPitch = kDim + 4;  // halves per row of the LDS key-centroid table (66 dwords: 8-byte reads spread over the banks)
 constexpr int kRowPad = 8;         // bytes after each staged payload row (34-dword rows for 128-byte payloads)
 
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 typedef short short4_t __attribute__((ext_vector_type(4)));
@@ -400,11 +401,12 @@ __device__ __forceinline__ void residual_h(const StageView<F>& S, int t, int g, 
     }
 }
 
-// Quantised residuals in fp32, value m of the lane's channels.
-template <int F>
+// Quantised residuals in fp32, value m of the lane's channels (the codes
+// times the token's scale, or the bare codes when SCALED is false).
+template <int F, bool SCALED = true>
 __device__ __forceinline__ void residual_f(const StageView<F>& S, int t, int g, float* r) {
     const uint8_t* row = S.row(t);
-    const float s = S.scale(t);
+    const float s = SCALED ? S.scale(t) : 1.0f;
     if constexpr (F == D_Q4 || F == D_Q2) {
         // signed codes, channel d in word d / (32/bits) at bit (d % (32/bits)) * bits (reference.py:17-21)
         constexpr int bits = F == D_Q4 ? 4 : 2;
@@ -439,6 +441,56 @@ __device__ __forceinline__ void residual_f(const StageView<F>& S, int t, int g, 
     }
 }
 
+// Signed INT4 / INT2 codes of the lane's channel pairs as exact fp16 pairs
+// (h[i] = values 2i, 2i + 1), without the scale.  Codes are biased to
+// unsigned fields by flipping their sign bits (u = code + 2^(bits-1)).  One
+// byte permute copies the pair's byte under an fp16 high byte 0x64 into both
+// halves (0x64bb: 1024 + bb, ulp 1); a mask keeps one field per half, which
+// then reads 1024 + u * 2^k for the field's bit offset k within the byte; one
+// packed fp16 FMA scales by 2^-k and subtracts 1024 / 2^k + 2^(bits-1),
+// leaving the code.  Every step is exact.
+template <int F>
+__device__ __forceinline__ void code_halves(const StageView<F>& S, int t, int g, uint32_t* h) {
+    const uint32_t* qw = reinterpret_cast<const uint32_t*>(S.row(t));
+    constexpr uint32_t kMagic = 0x64646464u;
+    if constexpr (F == D_Q4) {
+        // channel d in word d / 8 at bits 4 (d % 8): pair i of a word is its
+        // byte i, low nibble first (reference.py:17-21); words 2g, 2g + 1 hold
+        // channels 16g..16g+15 and words 8 + 2g, 9 + 2g channels 64+16g..64+16g+15
+        const half2_t mul = {(_Float16)1.0f, (_Float16)0.0625f}, add = {(_Float16)-1032.0f, (_Float16)-72.0f};
+        const uint2 a = *reinterpret_cast<const uint2*>(qw + 2 * g);
+        const uint2 b = *reinterpret_cast<const uint2*>(qw + 8 + 2 * g);
+        const uint32_t w[4] = {a.x, a.y, b.x, b.y};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t x = w[k] ^ 0x88888888u;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t d = __builtin_amdgcn_perm(kMagic, x, 0x04000400u + 0x00010001u * (uint32_t)j);
+                const half2_t e = __builtin_bit_cast(half2_t, d & 0xFFF0FF0Fu);  // 1024 + u0 | 1024 + 16 u1
+                h[4 * k + j] = __builtin_bit_cast(uint32_t, e * mul + add);
+            }
+        }
+    } else {
+        // channel d in word d / 16 at bits 2 (d % 16): pair p of a word is its
+        // nibble p; word g holds channels 16g..16g+15, word 4 + g 64+16g..
+        const half2_t mul_e = {(_Float16)1.0f, (_Float16)0.25f}, add_e = {(_Float16)-1026.0f, (_Float16)-258.0f};
+        const half2_t mul_o = {(_Float16)0.0625f, (_Float16)0.015625f}, add_o = {(_Float16)-66.0f, (_Float16)-18.0f};
+        const uint32_t w[2] = {qw[g], qw[4 + g]};
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const uint32_t x = w[k] ^ 0xAAAAAAAAu;
+#pragma unroll
+            for (int p = 0; p < 8; ++p) {
+                const uint32_t d = __builtin_amdgcn_perm(kMagic, x, 0x04000400u + 0x00010001u * (uint32_t)(p >> 1));
+                // even nibble: fields at bits 0-1 and 2-3 of the byte; odd: 4-5 and 6-7
+                const half2_t e = __builtin_bit_cast(half2_t, d & ((p & 1) ? 0xFFC0FF30u : 0xFF0CFF03u));
+                h[8 * k + p] = __builtin_bit_cast(uint32_t, (p & 1) ? e * mul_o + add_o : e * mul_e + add_e);
+            }
+        }
+    }
+}
+
 // Key values of the lane's 32 channels (pre-RoPE, fp32): centroid + residual.
 // fp16 + fp16 (or fp16 + fp32) sums run as one mixed-precision FMA by `one`.
 template <int F>
@@ -466,6 +518,16 @@ __device__ __forceinline__ void key_values(const StageView<F>& S, int t, int g, 
                 x[2 * i + 1] = half_hi(h[i]);
             }
         }
+    } else if constexpr (F == D_Q4 || F == D_Q2) {
+        // code * scale + centroid: one mixed-precision FMA per channel
+        uint32_t h[16];
+        code_halves<F>(S, t, g, h);
+        const float sc = S.scale(t);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            x[2 * i] = __builtin_fmaf(half_lo(h[i]), sc, half_lo(c[i]));
+            x[2 * i + 1] = __builtin_fmaf(half_hi(h[i]), sc, half_hi(c[i]));
+        }
     } else {
         float r[32];
         residual_f<F>(S, t, g, r);
@@ -478,16 +540,19 @@ __device__ __forceinline__ void key_values(const StageView<F>& S, int t, int g, 
 }
 
 // Value residuals of the lane's 32 channels as fp16 pairs for the matrix cores.
-// FP16 formats hand their payload halves through unchanged; quantised codes
-// are dequantised in fp32 and rounded once to fp16.
+// FP16 formats hand their payload halves through unchanged.  Quantised
+// formats hand over their integer codes (exact in fp16); the token's scale
+// multiplies its softmax weight instead (the P x V operand is fp16(p * s)).
 template <int F>
 __device__ __forceinline__ void value_halves(const StageView<F>& S, int t, int g, int width, GroupMask gm,
                                              const uint32_t* lut, uint32_t* h) {
     if constexpr (kHalfFmt<F>) {
         residual_h<F>(S, t, g, width, gm, lut, h);
+    } else if constexpr (F == D_Q4 || F == D_Q2) {
+        code_halves<F>(S, t, g, h);
     } else {
         float r[32];
-        residual_f<F>(S, t, g, r);
+        residual_f<F, false>(S, t, g, r);
 #pragma unroll
         for (int i = 0; i < 16; ++i) h[i] = (uint32_t)f2h(r[2 * i]) | ((uint32_t)f2h(r[2 * i + 1]) << 16);
     }
@@ -557,9 +622,11 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
 
     uint16_t* s_cent = reinterpret_cast<uint16_t*>(smem);  // region 0: fp16 key centroids [nc][kCPitch]
     uint32_t* s_lut = reinterpret_cast<uint32_t*>(smem + P.lut_off);
-    // per wave: fp16 weights [4-token group][head][token] and the V tile [token][kVPitch]
-    uint16_t* my_p = reinterpret_cast<uint16_t*>(smem + P.p_off) + wave * (kTile * G + kTile * kVPitch);
-    uint16_t* my_vt = my_p + kTile * G;
+    // per wave: fp16 weights [4-token group][head][token], the same times the
+    // tokens' V scales (scaled formats), and the V tile [token][kVPitch]
+    uint16_t* my_p = reinterpret_cast<uint16_t*>(smem + P.p_off) + wave * (2 * kTile * G + kTile * kVPitch);
+    uint16_t* my_ps = my_p + kTile * G;
+    uint16_t* my_vt = my_p + 2 * kTile * G;
     uint8_t* st_k = smem + P.stage_off + wave * (P.stage_k + P.stage_v);
     uint8_t* st_v = st_k + P.stage_k;
     const StageView<KF> SK{st_k, P.k.pb + kRowPad};
@@ -737,6 +804,7 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
         // ---- online softmax over the tile: one exponential per lane ----
         bool grow = false;
         float mnew[NH];
+        const float vscale = VT::SC ? SV.scale(stok) : 1.0f;  // V scale of this lane's score token
 #pragma unroll
         for (int hs = 0; hs < NH; ++hs) {
             const bool ok = stok < n && 4 * hs + hj < G;
@@ -769,7 +837,10 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
             const uint16_t ph = f2h(ok ? exp2_fast(sc[hs] - m_run[hs]) : 0.0f);
             const float pq = h2f(ph);
             lv[hs] += pq;
-            if (g < G) my_p[((((lane >> 2) & 3) * G + g) << 2) + (lane >> 4)] = ph;
+            const int pslot = ((((lane >> 2) & 3) * G + g) << 2) + (lane >> 4);
+            if (g < G) my_p[pslot] = ph;
+            if constexpr (VT::SC)
+                if (g < G) my_ps[pslot] = f2h(pq * vscale);
         }
         wave_sync();
 
@@ -800,10 +871,15 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
                 for (int hs = 0; hs < NH; ++hs) {
                     // A: lane 4b + i holds P[head 4 hs + i][tokens 4s + r]
                     const int g = 4 * hs + blk_row;
-                    half4_t a = (half4_t){0, 0, 0, 0};
+                    half4_t a = (half4_t){0, 0, 0, 0}, as = a;
                     if (g < G) a = __builtin_bit_cast(half4_t, *reinterpret_cast<const uint2*>(my_p + ((s * G + g) << 2)));
-                    acc[hs][0] = __builtin_amdgcn_mfma_f32_4x4x4f16(a, b0, acc[hs][0], 0, 0, 0);
-                    acc[hs][1] = __builtin_amdgcn_mfma_f32_4x4x4f16(a, b1, acc[hs][1], 0, 0, 0);
+                    if constexpr (VT::SC) {
+                        if (g < G) as = __builtin_bit_cast(half4_t, *reinterpret_cast<const uint2*>(my_ps + ((s * G + g) << 2)));
+                    } else {
+                        as = a;
+                    }
+                    acc[hs][0] = __builtin_amdgcn_mfma_f32_4x4x4f16(as, b0, acc[hs][0], 0, 0, 0);
+                    acc[hs][1] = __builtin_amdgcn_mfma_f32_4x4x4f16(as, b1, acc[hs][1], 0, 0, 0);
                     if constexpr (VT::CENT) accb[hs] = __builtin_amdgcn_mfma_f32_4x4x4f16(a, oh, accb[hs], 0, 0, 0);
                 }
             }
@@ -1351,7 +1427,7 @@ int run_decode(const void* q, int kf, const DTensor& k, int vf, const DTensor& v
     const int region0 = cent_bytes > merge_bytes ? cent_bytes : merge_bytes;
     p.lut_off = region0;
     p.p_off = p.lut_off + (kLutWords + kStructLutWords) * 4;
-    p.stage_off = p.p_off + kWaves * (kTile * G + kTile * kVPitch) * 2;
+    p.stage_off = p.p_off + kWaves * (2 * kTile * G + kTile * kVPitch) * 2;
     const size_t shm = (size_t)p.stage_off + (size_t)kWaves * (p.stage_k + p.stage_v);
     RESKV_REQUIRE(shm <= 160 * 1024, "decode LDS requirement %zu exceeds 160 KiB", shm);
     p.pm = (float*)ws;
