@@ -401,12 +401,11 @@ __device__ __forceinline__ void residual_h(const StageView<F>& S, int t, int g, 
     }
 }
 
-// Quantised residuals in fp32, value m of the lane's channels (the codes
-// times the token's scale, or the bare codes when SCALED is false).
-template <int F, bool SCALED = true>
+// Quantised residuals in fp32, value m of the lane's channels.
+template <int F>
 __device__ __forceinline__ void residual_f(const StageView<F>& S, int t, int g, float* r) {
     const uint8_t* row = S.row(t);
-    const float s = SCALED ? S.scale(t) : 1.0f;
+    const float s = S.scale(t);
     if constexpr (F == D_Q4 || F == D_Q2) {
         // signed codes, channel d in word d / (32/bits) at bit (d % (32/bits)) * bits (reference.py:17-21)
         constexpr int bits = F == D_Q4 ? 4 : 2;
@@ -540,19 +539,25 @@ __device__ __forceinline__ void key_values(const StageView<F>& S, int t, int g, 
 }
 
 // Value residuals of the lane's 32 channels as fp16 pairs for the matrix cores.
-// FP16 formats hand their payload halves through unchanged.  Quantised
-// formats hand over their integer codes (exact in fp16); the token's scale
-// multiplies its softmax weight instead (the P x V operand is fp16(p * s)).
+// FP16 formats hand their payload halves through unchanged.  Quantised codes
+// times the fp16 scale are rounded once to fp16: one packed fp16 multiply of
+// the exact codes for the unstructured formats, fp32 then a conversion for
+// the structured one.
 template <int F>
 __device__ __forceinline__ void value_halves(const StageView<F>& S, int t, int g, int width, GroupMask gm,
                                              const uint32_t* lut, uint32_t* h) {
     if constexpr (kHalfFmt<F>) {
         residual_h<F>(S, t, g, width, gm, lut, h);
     } else if constexpr (F == D_Q4 || F == D_Q2) {
-        code_halves<F>(S, t, g, h);
+        uint32_t c[16];
+        code_halves<F>(S, t, g, c);
+        const _Float16 sh = (_Float16)S.scale(t);  // the stored fp16 scale, exactly
+        const half2_t s2 = {sh, sh};
+#pragma unroll
+        for (int i = 0; i < 16; ++i) h[i] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, c[i]) * s2);
     } else {
         float r[32];
-        residual_f<F, false>(S, t, g, r);
+        residual_f<F>(S, t, g, r);
 #pragma unroll
         for (int i = 0; i < 16; ++i) h[i] = (uint32_t)f2h(r[2 * i]) | ((uint32_t)f2h(r[2 * i + 1]) << 16);
     }
@@ -622,11 +627,9 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
 
     uint16_t* s_cent = reinterpret_cast<uint16_t*>(smem);  // region 0: fp16 key centroids [nc][kCPitch]
     uint32_t* s_lut = reinterpret_cast<uint32_t*>(smem + P.lut_off);
-    // per wave: fp16 weights [4-token group][head][token], the same times the
-    // tokens' V scales (scaled formats), and the V tile [token][kVPitch]
-    uint16_t* my_p = reinterpret_cast<uint16_t*>(smem + P.p_off) + wave * (2 * kTile * G + kTile * kVPitch);
-    uint16_t* my_ps = my_p + kTile * G;
-    uint16_t* my_vt = my_p + 2 * kTile * G;
+    // per wave: fp16 weights [4-token group][head][token] and the V tile [token][kVPitch]
+    uint16_t* my_p = reinterpret_cast<uint16_t*>(smem + P.p_off) + wave * (kTile * G + kTile * kVPitch);
+    uint16_t* my_vt = my_p + kTile * G;
     uint8_t* st_k = smem + P.stage_off + wave * (P.stage_k + P.stage_v);
     uint8_t* st_v = st_k + P.stage_k;
     const StageView<KF> SK{st_k, P.k.pb + kRowPad};
@@ -804,7 +807,6 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
         // ---- online softmax over the tile: one exponential per lane ----
         bool grow = false;
         float mnew[NH];
-        const float vscale = VT::SC ? SV.scale(stok) : 1.0f;  // V scale of this lane's score token
 #pragma unroll
         for (int hs = 0; hs < NH; ++hs) {
             const bool ok = stok < n && 4 * hs + hj < G;
@@ -837,10 +839,7 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
             const uint16_t ph = f2h(ok ? exp2_fast(sc[hs] - m_run[hs]) : 0.0f);
             const float pq = h2f(ph);
             lv[hs] += pq;
-            const int pslot = ((((lane >> 2) & 3) * G + g) << 2) + (lane >> 4);
-            if (g < G) my_p[pslot] = ph;
-            if constexpr (VT::SC)
-                if (g < G) my_ps[pslot] = f2h(pq * vscale);
+            if (g < G) my_p[((((lane >> 2) & 3) * G + g) << 2) + (lane >> 4)] = ph;
         }
         wave_sync();
 
@@ -871,15 +870,10 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
                 for (int hs = 0; hs < NH; ++hs) {
                     // A: lane 4b + i holds P[head 4 hs + i][tokens 4s + r]
                     const int g = 4 * hs + blk_row;
-                    half4_t a = (half4_t){0, 0, 0, 0}, as = a;
+                    half4_t a = (half4_t){0, 0, 0, 0};
                     if (g < G) a = __builtin_bit_cast(half4_t, *reinterpret_cast<const uint2*>(my_p + ((s * G + g) << 2)));
-                    if constexpr (VT::SC) {
-                        if (g < G) as = __builtin_bit_cast(half4_t, *reinterpret_cast<const uint2*>(my_ps + ((s * G + g) << 2)));
-                    } else {
-                        as = a;
-                    }
-                    acc[hs][0] = __builtin_amdgcn_mfma_f32_4x4x4f16(as, b0, acc[hs][0], 0, 0, 0);
-                    acc[hs][1] = __builtin_amdgcn_mfma_f32_4x4x4f16(as, b1, acc[hs][1], 0, 0, 0);
+                    acc[hs][0] = __builtin_amdgcn_mfma_f32_4x4x4f16(a, b0, acc[hs][0], 0, 0, 0);
+                    acc[hs][1] = __builtin_amdgcn_mfma_f32_4x4x4f16(a, b1, acc[hs][1], 0, 0, 0);
                     if constexpr (VT::CENT) accb[hs] = __builtin_amdgcn_mfma_f32_4x4x4f16(a, oh, accb[hs], 0, 0, 0);
                 }
             }
@@ -1427,7 +1421,7 @@ int run_decode(const void* q, int kf, const DTensor& k, int vf, const DTensor& v
     const int region0 = cent_bytes > merge_bytes ? cent_bytes : merge_bytes;
     p.lut_off = region0;
     p.p_off = p.lut_off + (kLutWords + kStructLutWords) * 4;
-    p.stage_off = p.p_off + kWaves * (2 * kTile * G + kTile * kVPitch) * 2;
+    p.stage_off = p.p_off + kWaves * (kTile * G + kTile * kVPitch) * 2;
     const size_t shm = (size_t)p.stage_off + (size_t)kWaves * (p.stage_k + p.stage_v);
     RESKV_REQUIRE(shm <= 160 * 1024, "decode LDS requirement %zu exceeds 160 KiB", shm);
     p.pm = (float*)ws;
