@@ -996,16 +996,34 @@ __device__ __forceinline__ float block_sum_nt(float v, float* red) {
 // and the fused split merge, which both call this, agree bit for bit.
 template <int NT>
 __device__ float recent_join(float oc, float cm, float cl, const RecentArgs& r, const float* scores, long bq,
-                             long bh, float* s_q, float* s_p, float* s_red) {
+                             long bh, float* s_q, float* s_p, float* s_red, uint4* s_v) {
 #pragma clang fp contract(off)
     const int tid = threadIdx.x;
     const bool row = tid < kRecentThreads;
     if (scores == nullptr && tid < kDim) s_q[tid] = h2f(r.q_rope[bq * kDim + tid]) * r.scaling;
     __syncthreads();
     float m = -INFINITY, l = 0.0f, acc = 0.0f;  // acc: channel tid
+    constexpr int kVPer = kRecentThreads * (kDim / 8) / NT;  // 16-byte pieces of a chunk's V rows per thread
     for (int c0 = 0; c0 < r.Tr; c0 += kRecentThreads) {
         const int t = c0 + tid;
         const bool live = row && t < r.Tr;
+        // the chunk's V rows into LDS with 16-byte loads by every thread (one
+        // round trip), read from LDS by the weighted sum below
+        {
+            const int pieces = min(kRecentThreads, r.Tr - c0) * (kDim / 8);
+            const uint4* vsrc = reinterpret_cast<const uint4*>(r.v + (bh * r.rs + c0) * kDim);
+            uint4 vrow[kVPer];
+#pragma unroll
+            for (int i = 0; i < kVPer; ++i) {
+                const int e = tid + NT * i;
+                vrow[i] = e < pieces ? vsrc[e] : make_uint4(0u, 0u, 0u, 0u);
+            }
+#pragma unroll
+            for (int i = 0; i < kVPer; ++i) {
+                const int e = tid + NT * i;
+                if (e < pieces) s_v[e] = vrow[i];
+            }
+        }
         float s = -INFINITY;
         if (live) {
             if (scores != nullptr) {
@@ -1026,7 +1044,7 @@ __device__ float recent_join(float oc, float cm, float cl, const RecentArgs& r, 
                 s = d;
             }
         }
-        const float mn = fmaxf(m, block_max_nt<NT>(s, s_red));
+        const float mn = fmaxf(m, block_max_nt<NT>(s, s_red));  // its barriers also publish s_v
         const float p = live ? expf(s - mn) : 0.0f;
         if (row) s_p[tid] = p;
         const float ps = block_sum_nt<NT>(p, s_red);  // its barriers also publish s_p
@@ -1034,13 +1052,13 @@ __device__ float recent_join(float oc, float cm, float cl, const RecentArgs& r, 
         l = fmaf(l, alpha, ps);
         if (tid < kDim) {
             const int n = min(kRecentThreads, r.Tr - c0);
-            const uint16_t* vr = r.v + (bh * r.rs + c0) * kDim + tid;
+            const uint16_t* vr = reinterpret_cast<const uint16_t*>(s_v) + tid;
             float a = 0.0f;
-            for (int j = 0; j < n; ++j) a = fmaf(s_p[j], h2f(vr[(long)j * kDim]), a);
+            for (int j = 0; j < n; ++j) a = fmaf(s_p[j], h2f(vr[j * kDim]), a);
             acc = fmaf(acc, alpha, a);
         }
         m = mn;
-        __syncthreads();  // s_p reads done before the next chunk writes it
+        __syncthreads();  // s_p and s_v reads done before the next chunk writes them
     }
     const float jm = fmaxf(cm, m);
     const float wc = cl > 0.0f ? __fmul_rn(cl, expf(cm - jm)) : 0.0f;
@@ -1052,18 +1070,30 @@ __device__ float recent_join(float oc, float cm, float cl, const RecentArgs& r, 
 
 // RECENT: the compressed result, rounded to fp16 as the unfused path stores
 // it, is joined with the recent tokens of `rc` before it is written.
+// LDS of the split merge: the Value centroids, split weights and the two
+// group-partial tables are dead once the compressed result is formed, so the
+// recent join's staged V rows (128 tokens x 256 B) reuse the same bytes.
+constexpr int kMergeVcBytes = kMaxClusters * kDim * 2;
+constexpr int kMergeWOff = kMergeVcBytes;
+constexpr int kMergeDOff = kMergeWOff + kMaxSplits * 4;
+constexpr int kMergeBOff = kMergeDOff + 8 * kDim * 4;
+constexpr int kMergeEnd = kMergeBOff + 16 * kMaxClusters * 4;
+constexpr int kRecentVBytes = kRecentThreads * kDim * 2;
+constexpr int kMergePool = kMergeEnd > kRecentVBytes ? kMergeEnd : kRecentVBytes;
+
 template <bool RECENT>
 __global__ void __launch_bounds__(kMergeThreads) decode_merge_kernel(
     const float* __restrict__ pm, const float* __restrict__ pl, const float* __restrict__ pdelta,
     const float* __restrict__ pbeta, const uint16_t* __restrict__ vcent, int vnc, int vcs, int Hq, int H,
     int splits, uint16_t* __restrict__ out, float* __restrict__ om, float* __restrict__ ol, RecentArgs rc) {
 #pragma clang fp contract(off)  // every product and sum as written (FMAs are explicit)
-    __shared__ float s_w[kMaxSplits];
+    __shared__ __align__(16) uint8_t s_pool[RECENT ? kMergePool : kMergeEnd];
+    uint4* s_vc = reinterpret_cast<uint4*>(s_pool);  // fp16 Value centroids [c][128]
+    float* s_w = reinterpret_cast<float*>(s_pool + kMergeWOff);
+    float4 (*s_d)[kDim / 4] = reinterpret_cast<float4 (*)[kDim / 4]>(s_pool + kMergeDOff);
+    float4 (*s_b)[kMaxClusters / 4] = reinterpret_cast<float4 (*)[kMaxClusters / 4]>(s_pool + kMergeBOff);
     __shared__ float s_red[kMergeThreads / kWave];
-    __shared__ float4 s_d[8][kDim / 4];
-    __shared__ float4 s_b[16][kMaxClusters / 4];
     __shared__ float s_beta[kMaxClusters];
-    __shared__ uint4 s_vc[kMaxClusters * kDim / 8];  // fp16 Value centroids [c][128]
     __shared__ float s_q[RECENT ? kDim : 1];
     __shared__ float s_p[RECENT ? kRecentThreads : 1];
     const long bq = blockIdx.x;  // b * Hq + hq
@@ -1208,8 +1238,9 @@ __global__ void __launch_bounds__(kMergeThreads) decode_merge_kernel(
     }
     if constexpr (RECENT) {
         // the same rounded product as the m the unfused merge stores (no contraction into cm - jm)
+        __syncthreads();  // the centroid fold's LDS reads are done before the join overwrites the pool
         const float r = recent_join<kMergeThreads>(h2f(oc), __fmul_rn(mx, kLn2), lsum, rc, nullptr, bq, bh, s_q, s_p,
-                                                   s_red);
+                                                   s_red, reinterpret_cast<uint4*>(s_pool));
         if (tid < kDim) out[bq * kDim + tid] = f2h(r);
     }
 }
@@ -1229,6 +1260,7 @@ __global__ void __launch_bounds__(kMergeThreads) merge_recent_kernel(
     __shared__ float s_q[kDim];
     __shared__ float s_p[kRecentThreads];
     __shared__ float s_red[kMergeThreads / kWave];
+    __shared__ uint4 s_rv[kRecentThreads * kDim / 8];  // a chunk of recent V rows
     const long bq = blockIdx.x;
     const int tid = threadIdx.x;
     const int G = Hq / H;
@@ -1236,7 +1268,7 @@ __global__ void __launch_bounds__(kMergeThreads) merge_recent_kernel(
     const long bh = b * H + hq / G;
     const RecentArgs r{q_rope, k_recent, v_recent, Tr, rs, scaling};
     const float oc = tid < kDim ? h2f(comp_out[bq * kDim + tid]) : 0.0f;
-    const float res = recent_join<kMergeThreads>(oc, comp_m[bq], comp_l[bq], r, scores, bq, bh, s_q, s_p, s_red);
+    const float res = recent_join<kMergeThreads>(oc, comp_m[bq], comp_l[bq], r, scores, bq, bh, s_q, s_p, s_red, s_rv);
     if (tid < kDim) out[bq * kDim + tid] = f2h(res);
 }
 
