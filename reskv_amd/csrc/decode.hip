@@ -986,21 +986,52 @@ __device__ __forceinline__ float block_sum_nt(float v, float* red) {
     return v;
 }
 
+// Chunk-0 operands of the recent join that a kernel may fetch before its
+// other work: the rotated query value of thread tid < 128, and half a K row:
+// thread tid holds token tid % 128, channels 64 (tid / 128) .. +63.
+struct RecentPre {
+    uint4 k[kDim / 16];
+    float q;
+    bool have;
+};
+
+__device__ __forceinline__ void recent_prefetch(const RecentArgs& r, const float* scores, long bq, long bh,
+                                                RecentPre& pre) {
+    const int tid = threadIdx.x;
+    const int t = tid & (kRecentThreads - 1), half = tid / kRecentThreads;
+    pre.have = scores == nullptr;
+    pre.q = 0.0f;
+    const uint4 zero = make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+    for (int i = 0; i < kDim / 16; ++i) pre.k[i] = zero;
+    if (!pre.have || r.Tr <= 0) return;
+    if (tid < kDim) pre.q = h2f(r.q_rope[bq * kDim + tid]);
+    if (t < r.Tr) {
+        const uint4* kr = reinterpret_cast<const uint4*>(r.k + (bh * r.rs + t) * kDim) + (kDim / 16) * half;
+#pragma unroll
+        for (int i = 0; i < kDim / 16; ++i) pre.k[i] = kr[i];
+    }
+}
+
 // Joint softmax (natural-log units) of the compressed result of row bq --
 // channel value oc of thread tid < 128, maximum cm, normaliser cl -- with its
-// Tr recent tokens, by an NT-thread workgroup.  The tokens are taken in chunks
-// of 128: threads 0..127 score token c0 + tid (given fp32 scores, or a
-// 128-dim dot product with the scaled rotated query) and own channel tid of
-// the weighted value sum; chunks combine by online rescaling.  Every sum is
-// written as an explicit FMA or rounded product, so the merge_recent kernel
-// and the fused split merge, which both call this, agree bit for bit.
+// Tr recent tokens, by a 256-thread workgroup.  The tokens are taken in chunks
+// of 128: token c0 + j is scored from given fp32 scores, or as a 128-dim dot
+// product with the scaled rotated query whose two 64-channel halves threads j
+// and j + 128 form; threads 0..127 own channel tid of the weighted value sum;
+// chunks combine by online rescaling.  Every sum is written as an explicit
+// FMA or rounded product, so the merge_recent kernel and the fused split
+// merge, which both call this, agree bit for bit.  `pre` may hold the first
+// chunk's query and K halves (recent_prefetch).
 template <int NT>
 __device__ float recent_join(float oc, float cm, float cl, const RecentArgs& r, const float* scores, long bq,
-                             long bh, float* s_q, float* s_p, float* s_red, uint4* s_v) {
+                             long bh, float* s_q, float* s_p, float* s_red, uint4* s_v, const RecentPre& pre) {
 #pragma clang fp contract(off)
+    static_assert(NT == 2 * kRecentThreads, "two threads per recent token");
     const int tid = threadIdx.x;
     const bool row = tid < kRecentThreads;
-    if (scores == nullptr && tid < kDim) s_q[tid] = h2f(r.q_rope[bq * kDim + tid]) * r.scaling;
+    const int half = tid / kRecentThreads;
+    if (scores == nullptr && tid < kDim) s_q[tid] = (pre.have ? pre.q : h2f(r.q_rope[bq * kDim + tid])) * r.scaling;
     __syncthreads();
     float m = -INFINITY, l = 0.0f, acc = 0.0f;  // acc: channel tid
     constexpr int kVPer = kRecentThreads * (kDim / 8) / NT;  // 16-byte pieces of a chunk's V rows per thread
@@ -1025,26 +1056,36 @@ __device__ float recent_join(float oc, float cm, float cl, const RecentArgs& r, 
             }
         }
         float s = -INFINITY;
-        if (live) {
-            if (scores != nullptr) {
-                s = scores[bq * r.Tr + t];
+        if (scores != nullptr) {
+            if (live) s = scores[bq * r.Tr + t];
+        } else {
+            // half a dot product per thread: token c0 + tid % 128, channels 64 half .. +63
+            const int th = c0 + (tid & (kRecentThreads - 1));
+            uint4 kw[kDim / 16];
+            if (pre.have && c0 == 0) {
+#pragma unroll
+                for (int i = 0; i < kDim / 16; ++i) kw[i] = pre.k[i];
             } else {
-                const uint4* kr = reinterpret_cast<const uint4*>(r.k + (bh * r.rs + t) * kDim);
-                float d = 0.0f;
+                const uint4* kr = reinterpret_cast<const uint4*>(r.k + (bh * r.rs + th) * kDim) + (kDim / 16) * half;
 #pragma unroll
-                for (int i = 0; i < kDim / 8; ++i) {
-                    const uint4 w = kr[i];
-                    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        d = fmaf(s_q[8 * i + 2 * j], h2f((uint16_t)(ws[j] & 0xFFFFu)), d);
-                        d = fmaf(s_q[8 * i + 2 * j + 1], h2f((uint16_t)(ws[j] >> 16)), d);
-                    }
-                }
-                s = d;
+                for (int i = 0; i < kDim / 16; ++i) kw[i] = th < r.Tr ? kr[i] : make_uint4(0u, 0u, 0u, 0u);
             }
+            const float* q = s_q + (kDim / 2) * half;
+            float d = 0.0f;
+#pragma unroll
+            for (int i = 0; i < kDim / 16; ++i) {
+                const uint32_t ws[4] = {kw[i].x, kw[i].y, kw[i].z, kw[i].w};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    d = fmaf(q[8 * i + 2 * j], h2f((uint16_t)(ws[j] & 0xFFFFu)), d);
+                    d = fmaf(q[8 * i + 2 * j + 1], h2f((uint16_t)(ws[j] >> 16)), d);
+                }
+            }
+            s_p[tid] = d;
+            __syncthreads();
+            if (live) s = s_p[tid] + s_p[tid + kRecentThreads];
         }
-        const float mn = fmaxf(m, block_max_nt<NT>(s, s_red));  // its barriers also publish s_v
+        const float mn = fmaxf(m, block_max_nt<NT>(s, s_red));  // its barriers also publish s_v (and end the s_p reads)
         const float p = live ? expf(s - mn) : 0.0f;
         if (row) s_p[tid] = p;
         const float ps = block_sum_nt<NT>(p, s_red);  // its barriers also publish s_p
@@ -1068,8 +1109,6 @@ __device__ float recent_join(float oc, float cm, float cl, const RecentArgs& r, 
     return __fmul_rn(fmaf(oc, wc, __fmul_rn(acc, wr)), inv);
 }
 
-// RECENT: the compressed result, rounded to fp16 as the unfused path stores
-// it, is joined with the recent tokens of `rc` before it is written.
 // LDS of the split merge: the Value centroids, split weights and the two
 // group-partial tables are dead once the compressed result is formed, so the
 // recent join's staged V rows (128 tokens x 256 B) reuse the same bytes.
@@ -1081,6 +1120,9 @@ constexpr int kMergeEnd = kMergeBOff + 16 * kMaxClusters * 4;
 constexpr int kRecentVBytes = kRecentThreads * kDim * 2;
 constexpr int kMergePool = kMergeEnd > kRecentVBytes ? kMergeEnd : kRecentVBytes;
 
+// RECENT: the compressed result, rounded to fp16 as the unfused path stores
+// it, is joined with the recent tokens of `rc` before it is written; the
+// join's first query and K rows are fetched before the split merge starts.
 template <bool RECENT>
 __global__ void __launch_bounds__(kMergeThreads) decode_merge_kernel(
     const float* __restrict__ pm, const float* __restrict__ pl, const float* __restrict__ pdelta,
@@ -1095,7 +1137,7 @@ __global__ void __launch_bounds__(kMergeThreads) decode_merge_kernel(
     __shared__ float s_red[kMergeThreads / kWave];
     __shared__ float s_beta[kMaxClusters];
     __shared__ float s_q[RECENT ? kDim : 1];
-    __shared__ float s_p[RECENT ? kRecentThreads : 1];
+    __shared__ float s_p[RECENT ? 2 * kRecentThreads : 1];
     const long bq = blockIdx.x;  // b * Hq + hq
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int G = Hq / H;
@@ -1108,6 +1150,8 @@ __global__ void __launch_bounds__(kMergeThreads) decode_merge_kernel(
     const float4* bbase = reinterpret_cast<const float4*>(pbeta + (bq * splits) * kMaxClusters) + bq4;
     const float4 zero4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 
+    RecentPre pre;
+    if constexpr (RECENT) recent_prefetch(rc, nullptr, bq, bh, pre);
     // 0) loads that do not depend on the split weights
     const bool one_pass = splits <= kMergeThreads;  // one split per thread for the maximum and weights
     float m0 = -INFINITY, l0 = 0.0f;
@@ -1240,7 +1284,7 @@ __global__ void __launch_bounds__(kMergeThreads) decode_merge_kernel(
         // the same rounded product as the m the unfused merge stores (no contraction into cm - jm)
         __syncthreads();  // the centroid fold's LDS reads are done before the join overwrites the pool
         const float r = recent_join<kMergeThreads>(h2f(oc), __fmul_rn(mx, kLn2), lsum, rc, nullptr, bq, bh, s_q, s_p,
-                                                   s_red, reinterpret_cast<uint4*>(s_pool));
+                                                   s_red, reinterpret_cast<uint4*>(s_pool), pre);
         if (tid < kDim) out[bq * kDim + tid] = f2h(r);
     }
 }
@@ -1258,7 +1302,7 @@ __global__ void __launch_bounds__(kMergeThreads) merge_recent_kernel(
     uint16_t* __restrict__ out) {
 #pragma clang fp contract(off)
     __shared__ float s_q[kDim];
-    __shared__ float s_p[kRecentThreads];
+    __shared__ float s_p[2 * kRecentThreads];
     __shared__ float s_red[kMergeThreads / kWave];
     __shared__ uint4 s_rv[kRecentThreads * kDim / 8];  // a chunk of recent V rows
     const long bq = blockIdx.x;
@@ -1268,7 +1312,10 @@ __global__ void __launch_bounds__(kMergeThreads) merge_recent_kernel(
     const long bh = b * H + hq / G;
     const RecentArgs r{q_rope, k_recent, v_recent, Tr, rs, scaling};
     const float oc = tid < kDim ? h2f(comp_out[bq * kDim + tid]) : 0.0f;
-    const float res = recent_join<kMergeThreads>(oc, comp_m[bq], comp_l[bq], r, scores, bq, bh, s_q, s_p, s_red, s_rv);
+    RecentPre pre;
+    recent_prefetch(r, scores, bq, bh, pre);
+    const float res = recent_join<kMergeThreads>(oc, comp_m[bq], comp_l[bq], r, scores, bq, bh, s_q, s_p, s_red, s_rv,
+                                                 pre);
     if (tid < kDim) out[bq * kDim + tid] = f2h(res);
 }
 
