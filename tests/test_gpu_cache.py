@@ -148,6 +148,33 @@ def test_step_decoder_one_merge_launch_equals_two(device, sparsity, ring_len):
     assert torch.equal(again, ref)
 
 
+def test_decode_recent_with_empty_window_reads_no_recent_pointers(device):
+    """reskv_decode_recent with Tr = 0 accepts null recent pointers (the C ABI's
+    check) and must not read them: the result is the compressed-only decode."""
+    import ctypes
+
+    from reskv_amd import _lib
+    from reskv_amd._extension import _rope, cache_descriptors
+
+    k, v = _inputs(384, device, seed=31, b=2, h=2)
+    cache = compress(k, v, ResKVKernelConfig(sparsity=0.5, num_clusters=8))
+    g = seeded(32)
+    q = torch.randn(2, 8, 1, 128, generator=g).half().to(device)
+    freq = (500000.0 ** (-torch.arange(64).float() / 64)).to(device)
+    kd, vd, keep = cache_descriptors(cache)
+    f, table = _rope(freq, 500000.0, q.device, 384)
+    L = _lib.lib()
+    out = torch.full((2 * 8, 128), float("nan"), dtype=torch.float16, device=device)
+    ws = torch.empty(L.reskv_decode_workspace_bytes(2, 8, 2, 384, 0), dtype=torch.uint8, device=device)
+    stream = torch.cuda.current_stream(device).cuda_stream
+    _lib.check(L.reskv_decode_recent(q.data_ptr(), ctypes.byref(kd), ctypes.byref(vd), f.data_ptr(), table.data_ptr(),
+                                     2, 8, 2, 384, 0, 390, 0.1, 0, None, None, None, 0, 0, out.data_ptr(),
+                                     ws.data_ptr(), ws.numel(), stream), "decode_recent")
+    torch.cuda.synchronize()
+    ref = attention(q, cache, position=390, inv_freq=freq, scaling=0.1)
+    assert torch.equal(out.view(2, 8, 1, 128), ref)
+
+
 def test_attend_with_a_ring_of_several_chunks(device):
     """recent_size 256 + group 64: the ring holds up to 320 tokens, read in place
     by the split merge's multi-chunk join; checked against the oracle."""
