@@ -30,8 +30,8 @@ extern "C" {
 /* Thread-local description of the last failure; "" when none. */
 const char* reskv_last_error(void);
 
-/* Library ABI version (bumped on any signature or struct change, or when
- * entry points are added); 4. */
+/* Library ABI version (bumped on any signature, struct or data-layout
+ * change, or when entry points are added); 5. */
 int reskv_abi_version(void);
 
 /* ------------------------------------------------------------------ *
@@ -189,10 +189,15 @@ int reskv_decode_rope(const void* q, const reskv_ctensor* k, const reskv_ctensor
                       int start_pos, int pos_q, float scaling, int splits, void* out, float* m,
                       float* l, void* workspace, int64_t workspace_bytes, void* stream);
 
-/* RoPE table for positions [0, count): fp32 [count][128], row p holding, for
- * i0 = 0, 4, ..., 60, cos(fl32(p * inv_freq[i0 + j])) for j = 0..3 followed by
- * the four sines.  Serves the same role as the rotary cos/sin cache that
- * reskv/models/llama.py reads from the model (position_embeddings). */
+/* RoPE table for positions [0, count), count a positive multiple of 16:
+ * count * 128 fp32 values in blocks of 16 positions.  For frequency index
+ * d = 16 g + 4 u + j (g, u, j < 4), cos(fl32(p * inv_freq[d])) is element j of
+ * the float4 at index 512 (p / 16) + 64 (2u) + 4 (p % 16) + g, and the sine
+ * the same element of the float4 at 512 (p / 16) + 64 (2u + 1) + 4 (p % 16) + g.
+ * (The decode reads, per instruction, one such float4 for 16 consecutive
+ * positions and 4 groups: at most two contiguous runs.)  Serves the same
+ * role as the rotary cos/sin cache that reskv/models/llama.py reads from the
+ * model (position_embeddings). */
 int reskv_rope_table(const float* inv_freq, int count, float* table, void* stream);
 
 /* Joint softmax of the compressed result with precomputed fp32 recent scores.

@@ -14,7 +14,7 @@ LIB_PATH = _HERE / "libreskv_hip.so"
 _vp, _i, _i64, _f = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float
 
 # reskv_abi_version() of the library these signatures describe
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 
 class CTensor(ctypes.Structure):

@@ -746,9 +746,12 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
         const int pos = P.start_pos + tb + min(t, n - 1);
         float4 tr[8];
         if constexpr (TAB) {
-            const float4* trow = P.rope + (long)pos * (kDim / 4) + 8 * grp;
+            // piece i of group g for position p sits at float4
+            // 512 (p / 16) + 64 i + 4 (p % 16) + g: one load instruction reads
+            // the tile's 16 positions x 4 groups as at most two contiguous runs
+            const float4* trow = P.rope + (long)(pos >> 4) * 512 + 4 * (pos & 15) + grp;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) tr[i] = trow[i];
+            for (int i = 0; i < 8; ++i) tr[i] = trow[64 * i];
         }
 
         // ---- keys: centroid + residual, rotated ----
@@ -1658,14 +1661,17 @@ __global__ void __launch_bounds__(256) rope_table_kernel(const float* __restrict
     const int pos = (int)(idx / kHalf), pair = (int)(idx % kHalf);
     float sn, cs;
     rope_sincos_fast(__fmul_rn((float)pos, inv_freq[pair]), sn, cs);
-    float* row = table + (long)pos * kDim + (pair >> 2) * 8;
-    row[pair & 3] = cs;
-    row[4 + (pair & 3)] = sn;
+    // pair 16 g + 4 u + j: cos in piece 2u, sin in piece 2u + 1 of group g;
+    // piece i of group g for position p is float4 512 (p / 16) + 64 i + 4 (p % 16) + g
+    const int g = pair >> 4, u = (pair >> 2) & 3, j = pair & 3;
+    float* cell = table + 4 * ((long)(pos >> 4) * 512 + 64 * (2 * u) + 4 * (pos & 15) + g) + j;
+    cell[0] = cs;
+    cell[4 * 64] = sn;
 }
 
 extern "C" int reskv_rope_table(const float* inv_freq, int count, float* table, void* stream) {
     RESKV_REQUIRE(inv_freq && table, "null pointer argument");
-    RESKV_REQUIRE(count > 0, "position count must be positive");
+    RESKV_REQUIRE(count > 0 && count % 16 == 0, "position count must be a positive multiple of 16");
     const long n = (long)count * kHalf;
     hipLaunchKernelGGL(rope_table_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
                        inv_freq, count, table);

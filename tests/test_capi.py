@@ -33,13 +33,13 @@ def test_library_exports_every_declared_symbol():
     for name in declared_functions():
         assert hasattr(lib, name), name
         assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
-    assert lib.reskv_abi_version() == _lib.ABI_VERSION == 4
+    assert lib.reskv_abi_version() == _lib.ABI_VERSION == 5
 
 
 def test_a_library_of_another_abi_version_is_refused(monkeypatch):
     monkeypatch.setattr(_lib, "_lib", None)
-    monkeypatch.setattr(_lib, "ABI_VERSION", 3)
-    with pytest.raises(RuntimeError, match="ABI version 4, this binding needs 3"):
+    monkeypatch.setattr(_lib, "ABI_VERSION", 4)
+    with pytest.raises(RuntimeError, match="ABI version 5, this binding needs 4"):
         _lib.lib()
     assert _lib._lib is None  # nothing half-loaded is kept
 
@@ -116,6 +116,16 @@ def test_linspace_rows_match_torch_and_the_oracle():
     assert "T >= C" in _err(lib.reskv_linspace_rows(3, 4, rows))
     assert "T >= C" in _err(lib.reskv_kmeans(ctypes.c_void_p(16), None, ctypes.c_void_p(16), ctypes.c_void_p(16),
                                               1, 3, 4, 1, 0, ctypes.c_void_p(256), 1 << 20, None))
+
+
+def test_rope_table_needs_whole_blocks_of_positions():
+    """The table stores positions in blocks of 16; a count that is not a
+    multiple of 16 is refused before any device call."""
+    lib = _lib.lib()
+    p = ctypes.c_void_p(16)
+    assert "null" in _err(lib.reskv_rope_table(None, 16, p, None))
+    for count in (0, 20, 1000):
+        assert "multiple of 16" in _err(lib.reskv_rope_table(p, count, p, None))
 
 
 def test_quantiser_argument_checks():
