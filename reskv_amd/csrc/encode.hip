@@ -310,14 +310,6 @@ __device__ __forceinline__ uint32_t search7(const uint32_t* p, int base, int nnz
     }
     return c4;
 }
-// Bit-7 flags of 4 bytes -> 4 bits in byte order.
-__device__ __forceinline__ uint32_t movemask4(uint32_t f) {
-    uint32_t t = f >> 7;  // bits 0, 8, 16, 24
-    t |= t >> 7;          // bits 0, 1 hold bytes 0, 1; bits 16, 17 hold bytes 2, 3
-    t |= t >> 14;
-    return t & 0xFu;
-}
-
 __global__ void __launch_bounds__(256) encode_bitmap4_kernel(EncSides S, int T, int nnz, int bh0) {
     __shared__ __align__(16) uint16_t s_rows[kWavesPerBlock][kBitmapDump + kWave];
     const int side = blockIdx.z;
@@ -408,10 +400,17 @@ __global__ void __launch_bounds__(256) encode_bitmap4_kernel(EncSides S, int T, 
         for (int i = 0; i < 8; ++i) eq[i] = i == top ? cleared : eq[i];
         --n_eq;
     }
-    // kept channels as a 32-bit mask, bit i = channel 32 q + i
+    // kept channels as a 32-bit mask, bit i = channel 32 q + i: the flag bytes
+    // (0 or 1 after the shift) of two dwords weighted by 1..128 in one pair of
+    // byte dot products give 8 mask bits
     uint32_t sel = 0;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) sel |= movemask4(gt[i] | eq[i]) << (4 * i);
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t lo = (gt[2 * j] | eq[2 * j]) >> 7, hi = (gt[2 * j + 1] | eq[2 * j + 1]) >> 7;
+        const uint32_t m = __builtin_amdgcn_udot4(lo, 0x08040201u, __builtin_amdgcn_udot4(hi, 0x80402010u, 0u, false),
+                                                  false);
+        sel |= m << (8 * j);
+    }
     // the token keeps exactly nnz channels; the bound check keeps the LDS row
     // writes inside the row regardless
     const int kept = __builtin_popcount(sel);
