@@ -22,6 +22,9 @@ Restated functions and the reference lines they follow (under
 * ``reconstruct``          -- reference.py:12-49
 * ``rotate``               -- reference.py:52-56
 * ``reference_attention``  -- reference.py:59-91
+* ``merge_recent``         -- attention.cu:598-663, cluster_mass.cu:1106-1169
+                              (joint softmax of an fp16 compressed result and
+                              its (m, l) with recent tokens)
 * ``kmeans``               -- compression.py:19-53 (Lloyd: linspace init,
                               assign-then-update, K keeps empty centres, V zeroes
                               them, ids from the last assignment)
@@ -45,7 +48,9 @@ How each function is pinned (tests/test_oracle.py):
   exactly, and the dropped channels are exactly the smallest |fp16(r)|;
 * attention: dense softmax closed form (one token -> output equals its value,
   equal scores -> mean), RoPE identities (relative-position invariance, norm
-  preservation, inverse rotation);
+  preservation, inverse rotation); ``merge_recent`` of the unrounded
+  compressed statistics equals ``reference_attention`` over the concatenated
+  tokens, and with no recent tokens returns the compressed result;
 * k-means, K: ids are argmin of exact (float64) distances, centres are member
   means, linspace initial indices, the constant-data known answer of
   tests/test_cuda.py:161-169;
@@ -344,6 +349,34 @@ def compressed_stats(q, k_dense, v_dense, *, position, start_position=0, freq=No
     m, l, e = softmax_stats(s)
     out = np.einsum("bht,bhtd->bhd", e, v) / l[..., None]
     return out, m, l
+
+
+def merge_recent(comp_out, comp_m, comp_l, scores, v_recent):
+    """Joint softmax of a compressed result with recent tokens (float64).
+
+    comp_out [B, Hq, 128] (the decode op's normalised output, which the
+    reference stores in fp16 before this step), comp_m / comp_l [B, Hq] (max
+    score and sum of exp(s - m) of the compressed part), scores [B, Hq, Tr]
+    (scaled recent scores), v_recent [B, Hq, Tr, 128] (already repeated over
+    the query group).  The reference accumulates comp_out * l and each recent
+    token's weighted value with online rescaling and divides by the joint
+    normaliser (attention.cu:598-663; the deferred family's merge_recent,
+    cluster_mass.cu:1106-1169, takes the same inputs with precomputed scores);
+    in exact arithmetic that is
+        (comp_out l e^(m - M) + sum_t e^(s_t - M) v_t) / (l e^(m - M) + sum_t e^(s_t - M)),
+    M = max(m, max_t s_t), evaluated here directly.
+    """
+    out = np.asarray(comp_out, dtype=np.float64)
+    m = np.asarray(comp_m, dtype=np.float64)
+    l = np.asarray(comp_l, dtype=np.float64)
+    s = np.asarray(scores, dtype=np.float64)
+    if s.shape[-1] == 0:
+        return out.copy()
+    big = np.maximum(m, s.max(-1))
+    wc = l * np.exp(m - big)
+    e = np.exp(s - big[..., None])
+    num = out * wc[..., None] + np.einsum("bht,bhtd->bhd", e, np.asarray(v_recent, dtype=np.float64))
+    return num / (wc + e.sum(-1))[..., None]
 
 
 # ---------------------------------------------------------------------------

@@ -36,6 +36,27 @@ def expected_attention(q, cache, *, position, start_position=0, inv_freq=None, r
                                  rope_theta=rope_theta, scaling=scaling, recent=rec)
 
 
+def expected_attention_two_step(q, cache, *, position, start_position=0, inv_freq=None, rope_theta=500000.0,
+                                scaling=None, recent=None):
+    """The reference's structure for a recent window: the compressed result is
+    an fp16 op output, then joined with the recent tokens (merge_recent).
+    Float64 [B, Hq, 1, 128]; without a window the same as expected_attention."""
+    if recent is None:
+        return expected_attention(q, cache, position=position, start_position=start_position, inv_freq=inv_freq,
+                                  rope_theta=rope_theta, scaling=scaling)
+    freq = None if inv_freq is None else np_(inv_freq)
+    qq = np_(q).astype(np.float64)
+    out, m, l = o.compressed_stats(qq, dense(cache.key), dense(cache.value), position=position,
+                                   start_position=start_position, freq=freq, rope_theta=rope_theta,
+                                   scaling=scaling)
+    out16 = out.astype(np.float16).astype(np.float64)
+    q_r, k_r, v_r = (np_(x).astype(np.float64) for x in recent)
+    g = q.shape[1] // k_r.shape[1]
+    scale = 128 ** -0.5 if scaling is None else scaling
+    scores = (q_r @ np.swapaxes(np.repeat(k_r, g, axis=1), -1, -2))[..., 0, :] * scale
+    return o.merge_recent(out16, m, l, scores, np.repeat(v_r, g, axis=1))[:, :, None]
+
+
 def seeded(seed):
     return torch.Generator().manual_seed(seed)
 

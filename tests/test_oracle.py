@@ -310,6 +310,27 @@ def test_attention_matches_explicit_softmax_and_stats():
     assert np.isclose(m[0, 0], s0.max()) and np.isclose(l[0, 0], np.exp(s0 - s0.max()).sum())
 
 
+def test_merge_recent_of_exact_statistics_equals_the_joint_softmax():
+    """merge_recent (attention.cu:598-663) restated: joining the unrounded
+    compressed (out, m, l) with recent tokens is the softmax over all tokens;
+    with no recent token it returns the compressed result."""
+    rng = np.random.default_rng(11)
+    q = rng.standard_normal((2, 8, 1, 128))
+    k = rng.standard_normal((2, 2, 23, 128)) * 2.0
+    v = rng.standard_normal((2, 2, 23, 128))
+    kr_ = rng.standard_normal((2, 2, 9, 128)) * 3.0
+    vr_ = rng.standard_normal((2, 2, 9, 128))
+    f = o.theta_frequencies(500000.0)
+    qr = o.rotate(q, np.array([40]), f)
+    full = o.reference_attention(q, k, v, position=40, start_position=5, freq=f, recent=(qr, kr_, vr_))
+    co, m, l = o.compressed_stats(q, k, v, position=40, start_position=5, freq=f)
+    krr, vrr = np.repeat(kr_, 4, axis=1), np.repeat(vr_, 4, axis=1)
+    scores = (qr @ np.swapaxes(krr, -1, -2))[..., 0, :] * 128 ** -0.5
+    got = o.merge_recent(co, m, l, scores, vrr)
+    assert np.abs(got - full[:, :, 0]).max() < 1e-12
+    assert np.array_equal(o.merge_recent(co, m, l, scores[..., :0], vrr[:, :, :0]), co)
+
+
 def test_attention_with_recent_equals_concatenation():
     rng = np.random.default_rng(4)
     q = rng.standard_normal((1, 4, 1, 128))
