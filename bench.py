@@ -13,7 +13,8 @@ call is reported next to it).  ``value`` = batch * steps / elapsed (tokens/s).
 The JSON line also carries the roofline of one decode-attention call
 (algorithmic compressed bytes per call / measured time per call vs 8 TB/s),
 a sweep over the batch sizes and sparsities of config 2 plus the dense fp16
-baseline at the same shapes, config 1 (prefill compression), config 3
+baseline at the same shapes (this build's dense HIP kernel, and torch's
+scaled_dot_product_attention for reference), config 1 (prefill compression), config 3
 (INT4/INT2 decode), a stated-length config-4 end-to-end decode (ResKV against
 dense fp16 KV), and a CPU baseline: the torch restatement of the reference's
 compress and attention (oracle/torch_checker.py) on this host's cores.
@@ -189,6 +190,42 @@ def measure_dense(torch, b, t, layers, steps, warmup, device):
     torch.cuda.empty_cache()
     return {"batch": b, "us_per_layer_step": per_call * 1e6, "achieved_GBps": nbytes / per_call / 1e9,
             "frac": nbytes / per_call / HBM_PEAK, "distinct_caches": n}
+
+
+def measure_sdpa(torch, b, t, layers, steps, device):
+    """torch's scaled_dot_product_attention on dense fp16 K/V (already rotated),
+    a reference point beside the dense HIP kernel.  The four query heads of a
+    KV head ride in the query-length axis ([B, 8, 4, 128] against [B, 8, T,
+    128]), the same product as grouped-query decode with K/V read once.  Only
+    the flash and memory-efficient backends are allowed; where neither takes
+    the call the result says why instead of a time.  Timed eagerly (events
+    around `steps` rounds of `layers` calls)."""
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    g = torch.Generator(device=device).manual_seed(44)
+    n = max(2, min(layers, (2 << 30) // (b * HK * t * D * 2 * 2)))
+    ks = [torch.randn(b, HK, t, D, device=device, dtype=torch.float16, generator=g) * 0.5 for _ in range(n)]
+    vs = [torch.randn(b, HK, t, D, device=device, dtype=torch.float16, generator=g) * 0.5 for _ in range(n)]
+    q = torch.randn(b, HK, HQ // HK, D, device=device, dtype=torch.float16, generator=g)
+    out = {"batch": b, "distinct_caches": n}
+
+    def step():
+        for i in range(layers):
+            torch.nn.functional.scaled_dot_product_attention(q, ks[i % n], vs[i % n])
+
+    try:
+        with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+            step()
+            torch.cuda.synchronize()
+            secs = eager_time(torch, step, steps)
+        per_call = secs / (steps * layers)
+        nbytes = algorithmic_bytes(None, b, t, 0, 0)
+        out.update({"us_per_layer_step": per_call * 1e6, "frac": nbytes / per_call / HBM_PEAK})
+    except RuntimeError as e:
+        out["error"] = str(e).splitlines()[0][:200]
+    del ks, vs
+    torch.cuda.empty_cache()
+    return out
 
 
 def measure_encoders(torch, device, reps=20):
@@ -534,7 +571,7 @@ def main():
     r = measure_point(torch, args.batch, args.seq_len, args.sparsity, args.layout, args.layers, args.steps,
                       args.warmup, args.splits, device, eager=True)
     print(json.dumps({"point": r}), flush=True)
-    sweep, dense = [], []
+    sweep, dense, sdpa = [], [], []
     if not args.no_sweep:
         for sparsity in (0.5, 0.75):
             for b in BATCHES:
@@ -547,6 +584,10 @@ def main():
             d = measure_dense(torch, b, args.seq_len, args.layers, max(5, args.steps // 2), 2, device)
             dense.append(d)
             print(json.dumps({"dense": d}), flush=True)
+        for b in BATCHES:
+            d = measure_sdpa(torch, b, args.seq_len, args.layers, max(3, args.steps // 4), device)
+            sdpa.append(d)
+            print(json.dumps({"torch_sdpa": d}), flush=True)
     encode = quant = None
     if not args.no_sweep:
         encode = measure_encoders(torch, device)
@@ -594,6 +635,8 @@ def main():
             "parallelism": "single GPU",
             "sweep": sweep,
             "dense_sweep": [{k: d[k] for k in ("batch", "us_per_layer_step", "frac")} for d in dense],
+            "torch_sdpa_fp16_sweep": [{k: d[k] for k in ("batch", "us_per_layer_step", "frac", "error") if k in d}
+                                      for d in sdpa],
             "config1_prefill_compression": encode,
             "config3_quantized_decode_b8_t16384": quant,
             "config4_end_to_end": e2e,
