@@ -459,7 +459,8 @@ def value_distances(x, centers):
     cn = half_norms(c).astype(np.float64)
     dot = x.astype(np.float64) @ np.swapaxes(c.astype(np.float64), -1, -2)
     d = xn[..., :, None] + cn[..., None, :] - 2.0 * dot
-    return _fp16_sqrt(d.astype(np.float16)), d
+    with np.errstate(over="ignore"):  # beyond 65504 the fp16 distance is inf, as in torch
+        return _fp16_sqrt(d.astype(np.float16)), d
 
 
 def assign_value(x, centers):
@@ -500,8 +501,9 @@ def value_ambiguous(x, centers, rel=2.0 ** -20):
     ulp = lambda v: np.abs(np.nextafter(v.astype(np.float16), np.float16(np.inf)).astype(np.float64)
                            - v.astype(np.float16).astype(np.float64))
     width = width + np.where(xamb, ulp(xs), 0.0)[..., :, None] + np.where(camb, ulp(cs), 0.0)[..., None, :]
-    lo = _fp16_sqrt((d - width).astype(np.float16)).astype(np.float64)
-    hi = _fp16_sqrt((d + width).astype(np.float16)).astype(np.float64)
+    with np.errstate(over="ignore"):
+        lo = _fp16_sqrt((d - width).astype(np.float16)).astype(np.float64)
+        hi = _fp16_sqrt((d + width).astype(np.float16)).astype(np.float64)
     w = np.argmin(s16.astype(np.float32), axis=-1)
     hw = np.take_along_axis(hi, w[..., None], axis=-1)
     idx = np.arange(c.shape[-2])
