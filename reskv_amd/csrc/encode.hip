@@ -248,10 +248,11 @@ __global__ void __launch_bounds__(256) encode_bitmap_kernel(
 // tokens).  The nnz-th largest 15-bit magnitude M is found bit by bit on byte
 // planes: a lane's 32 magnitudes are split into a plane of high bytes (bits
 // 14..8) and one of low bytes, four values per dword, byte k of dword i
-// holding channel 32 q + 4 i + k.  For byte values v, c <= 0x80,
-// ((v | 0x80) - c) & 0x80 is set exactly when v >= c and no borrow crosses a
-// byte, so one subtraction, one mask and one popcount count four values
-// against a candidate.  Phases:
+// holding channel 32 q + 4 i + k.  A search step counts the bytes >= a
+// candidate c with two sums of absolute byte differences (v_sad_u8, against
+// c and c - 1), four values an instruction; the per-channel flags after each
+// phase use ((v | 0x80) - c) & 0x80, set exactly when v >= c (v, c <= 0x80,
+// no borrow crosses a byte).  Phases:
 //   A: the high seven bits H of M over the high bytes;
 //   B: bits 7..1 of M (L) over the low bytes >> 1 of the values whose high
 //      byte is H (the others read as 0 and never count: candidates are >= 1),
@@ -285,28 +286,29 @@ __device__ __forceinline__ int quad_prefix(int v, int q) {
 }
 // Bit-7 flags of the bytes of p (each ORed with 0x80 beforehand) that are >= the bytes of c4.
 __device__ __forceinline__ uint32_t ge_flags(uint32_t p, uint32_t c4) { return (p - c4) & kByteTop; }
-// popcount(x) + acc as one v_bcnt_u32_b32 (the accumulate is the
-// instruction's own operand): written out so that a count over several words
-// stays a chain of these instead of being rebalanced into separate adds.
-__device__ __forceinline__ int bcnt_acc(uint32_t x, int acc) {
-    int r;
-    asm("v_bcnt_u32_b32 %0, %1, %2" : "=v"(r) : "v"(x), "v"(acc));
-    return r;
-}
-// Number of the lane's 32 plane bytes >= the bytes of c4.
-__device__ __forceinline__ int count_ge(const uint32_t* p, uint32_t c4) {
-    int n = 0;
+// Twice the number of the lane's 32 plane bytes (7-bit values, bit 7 clear)
+// that are >= the bytes of c4 (each 1..127), minus 32: for a byte a,
+// |a - c| - |a - (c - 1)| is -1 when a >= c and +1 otherwise, so two sums of
+// absolute byte differences (v_sad_u8, four bytes an instruction) give the
+// count without per-byte flags.
+__device__ __forceinline__ int twice_count_ge_minus(const uint32_t* p, uint32_t c4) {
+    uint32_t at = 0, below = 0;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) n = bcnt_acc(ge_flags(p[i], c4), n);
-    return n;
+    for (int i = 0; i < 8; ++i) {
+        at = __builtin_amdgcn_sad_u8(p[i], c4, at);
+        below = __builtin_amdgcn_sad_u8(p[i], c4 - kByteOne, below);
+    }
+    return (int)below - (int)at;  // = 2 * count - 32
 }
-// Largest 7-bit c (as four equal bytes) with base + (token count of plane bytes >= c) >= nnz.
+// Largest 7-bit c (as four equal bytes) with base + (token count of plane bytes >= c) >= nnz,
+// over planes of 7-bit values.
 __device__ __forceinline__ uint32_t search7(const uint32_t* p, int base, int nnz) {
+    const int need = 2 * (nnz - base) - 4 * 32;  // 2 * count - 128 over the quad's 128 bytes
     uint32_t c4 = 0;
 #pragma unroll
     for (int bit = 6; bit >= 0; --bit) {
         const uint32_t cand = c4 | (kByteOne << bit);
-        c4 = base + quad_sum(count_ge(p, cand)) >= nnz ? cand : c4;
+        c4 = quad_sum(twice_count_ge_minus(p, cand)) >= need ? cand : c4;
     }
     return c4;
 }
@@ -340,17 +342,19 @@ __global__ void __launch_bounds__(256) encode_bitmap4_kernel(EncSides S, int T, 
         for (int k = 0; k < 4; ++k)
             hp[4 * j + k] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, xw[k]) - __builtin_bit_cast(half2_t, cw[k]));
     }
-    // byte planes of the magnitudes (sign bits dropped): hb = bits 14..8, lb = bits 7..0
-    uint32_t hb[8], lb[8];
+    // byte planes of the magnitudes (sign bits dropped): hr = bits 14..8, lb =
+    // bits 7..0; hb = hr with bit 7 of every byte set, for the flag tests
+    uint32_t hr[8], hb[8], lb[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         const uint32_t m0 = hp[2 * i] & 0x7FFF7FFFu, m1 = hp[2 * i + 1] & 0x7FFF7FFFu;
-        hb[i] = __builtin_amdgcn_perm(m1, m0, 0x07050301u) | kByteTop;
+        hr[i] = __builtin_amdgcn_perm(m1, m0, 0x07050301u);
+        hb[i] = hr[i] | kByteTop;
         lb[i] = __builtin_amdgcn_perm(m1, m0, 0x06040200u);
     }
     // A: high byte H of M
-    const uint32_t h4 = search7(hb, 0, nnz);
-    uint32_t gt_h[8], eq_h[8], l7[8];
+    const uint32_t h4 = search7(hr, 0, nnz);
+    uint32_t gt_h[8], eq_h[8], l7r[8], l7[8];
     int above = 0;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -358,11 +362,12 @@ __global__ void __launch_bounds__(256) encode_bitmap4_kernel(EncSides S, int T, 
         eq_h[i] = ge_flags(hb[i], h4) & ~gt_h[i];
         above += __builtin_popcount(gt_h[i]);
         // bits 7..1 of the low byte where the high byte is H, else 0 (bytes of eq_h - (eq_h >> 7) are 0x7F or 0)
-        l7[i] = ((lb[i] >> 1) & (eq_h[i] - (eq_h[i] >> 7))) | kByteTop;
+        l7r[i] = (lb[i] >> 1) & (eq_h[i] - (eq_h[i] >> 7));
+        l7[i] = l7r[i] | kByteTop;
     }
     above = quad_sum(above);
     // B: bits 7..1 of M
-    const uint32_t l4 = search7(l7, above, nnz);
+    const uint32_t l4 = search7(l7r, above, nnz);
     uint32_t gt_l[8], eq_l[8], one[8];
     int above_l = 0, ones = 0;
 #pragma unroll
