@@ -155,9 +155,9 @@ def measure_point(torch, b, t, sparsity, layout, layers, steps, warmup, splits, 
         out["eager_us_per_layer_step"] = eager_time(torch, step, max(2, steps // 4)) / (max(2, steps // 4) * layers) * 1e6
     plan = caches[0].key.plan
     nbytes = algorithmic_bytes(plan, b, t, caches[0].key.centroids.shape[2], caches[0].value.centroids.shape[2])
-    from reskv_amd import _lib
+    from reskv_amd._extension import decode_splits
 
-    nsplit = _lib.lib().reskv_decode_splits(b, HQ, HK, t, splits)
+    nsplit = decode_splits(caches[0], HQ, splits)
     del caches
     torch.cuda.empty_cache()
     out.update({
@@ -318,9 +318,9 @@ def measure_point_bits(torch, b, t, bits, layers, steps, device):
     secs = graph_time(torch, step, steps, 2)
     per_call = secs / (steps * layers)
     nbytes = algorithmic_bytes(base.key.plan, b, t, 32, 32)
-    from reskv_amd import _lib
+    from reskv_amd._extension import decode_splits
 
-    nsplit = _lib.lib().reskv_decode_splits(b, HQ, HK, t, 0)
+    nsplit = decode_splits(caches[0], HQ)
     del caches
     torch.cuda.empty_cache()
     return {"us_per_layer_step": per_call * 1e6, "achieved_GBps": nbytes / per_call / 1e9,

@@ -31,7 +31,7 @@ extern "C" {
 const char* reskv_last_error(void);
 
 /* Library ABI version (bumped on any signature, struct or data-layout
- * change, or when entry points are added); 5. */
+ * change, or when entry points are added); 6. */
 int reskv_abi_version(void);
 
 /* ------------------------------------------------------------------ *
@@ -158,12 +158,18 @@ typedef struct reskv_ctensor {
                                 tables; 0 means nc (dense) */
 } reskv_ctensor;
 
-/* Bytes of split-K scratch reskv_decode needs; splits<=0 means automatic. */
+/* Bytes of split-K scratch a decode of these sizes needs, for every residual
+ * format (the automatic split count depends on the format; this covers the
+ * largest); splits<=0 means automatic. */
 int64_t reskv_decode_workspace_bytes(int B, int Hq, int H, int T, int splits);
 
-/* Split count reskv_decode will use for these sizes (splits<=0: automatic,
- * chosen from the 256-CU occupancy; >0: min(splits, T)). */
-int reskv_decode_splits(int B, int Hq, int H, int T, int splits);
+/* Split count a decode of these tensors makes (splits<=0: automatic, filling
+ * the 256 CUs with as many workgroups as the format's kernel keeps resident
+ * per CU, at least two 16-token tiles per wave; >0: min(splits, T, 1024)).
+ * rope_table: non-zero when the call passes a RoPE table.  Returns -1 (and
+ * sets reskv_last_error) on bad arguments. */
+int reskv_decode_splits(const reskv_ctensor* k, const reskv_ctensor* v, int rope_table, int B, int Hq, int H, int T,
+                        int splits);
 
 /* Decode one query token per (batch, query head) against the compressed cache.
  * Replaces the deferred ops ext.decode_fp16 / decode_structured_fp16 /

@@ -409,6 +409,17 @@ def cache_descriptors(cache):
     return out[0], out[1], tuple(keep)
 
 
+def decode_splits(cache, num_q_heads, splits=0, rope_table=True):
+    """Split count a decode of ``cache`` with ``num_q_heads`` query heads makes
+    (``splits`` = 0: automatic, from the format kernel's per-CU occupancy)."""
+    kdesc, vdesc, _keep = cache_descriptors(cache)
+    b, kh = cache.key.centroids.shape[:2]
+    n = _lib.lib().reskv_decode_splits(kdesc, vdesc, int(bool(rope_table)), b, int(num_q_heads), kh, cache.seq_len,
+                                       int(splits))
+    _lib.check(0 if n > 0 else 1, "decode_splits")
+    return n
+
+
 class StepDecoder:
     """Repeated decode steps of one layer against a fixed compressed history and
     a dense ring of recent tokens, without per-call validation or allocation.

@@ -14,7 +14,7 @@ LIB_PATH = _HERE / "libreskv_hip.so"
 _vp, _i, _i64, _f = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float
 
 # reskv_abi_version() of the library these signatures describe
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 
 class CTensor(ctypes.Structure):
@@ -53,7 +53,7 @@ SIGNATURES = {
     "reskv_kmeans_assign": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _vp, _i64, _vp]),
     "reskv_kmeans_kv": (_i, [_vp] * 8 + [_i, _i, _i, _i, _vp, _i64, _vp]),
     "reskv_decode_workspace_bytes": (_i64, [_i, _i, _i, _i, _i]),
-    "reskv_decode_splits": (_i, [_i, _i, _i, _i, _i]),
+    "reskv_decode_splits": (_i, [ctypes.POINTER(CTensor), ctypes.POINTER(CTensor), _i, _i, _i, _i, _i, _i]),
     "reskv_decode": (_i, [_vp, ctypes.POINTER(CTensor), ctypes.POINTER(CTensor), _vp, _i, _i, _i, _i, _i, _i,
                           _f, _i, _vp, _vp, _vp, _vp, _i64, _vp]),
     "reskv_decode_rope": (_i, [_vp, ctypes.POINTER(CTensor), ctypes.POINTER(CTensor), _vp, _vp, _i, _i, _i, _i,

@@ -1336,24 +1336,31 @@ __global__ void __launch_bounds__(kMergeThreads) merge_recent_kernel(
 // ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
-// Two 4-wave workgroups fit a CU at this kernel's register use, so about 512
-// workgroups fill the 256 CUs once; each wave keeps at least two 16-token
-// tiles so that its next tile's loads overlap the current tile's arithmetic.
-int auto_splits(int B, int H, int T) {
+// The automatic split count fills every CU with as many workgroups as the
+// kernel instance keeps resident per CU (two for most formats at their
+// register use, three for the quantised ones); each wave keeps at least two
+// 16-token tiles so that its next tile's loads overlap the current tile's
+// arithmetic.
+constexpr int kCUs = 256;            // compute units of an MI355X
+constexpr int kMaxGroupsPerCU = 4;   // cap of the automatic split target (and of the workspace bound)
+
+int auto_splits(int B, int H, int T, int per_cu) {
     const long heads = (long)B * H;
-    long s = (512 + heads - 1) / heads;
+    long s = ((long)per_cu * kCUs + heads - 1) / heads;
     const long cap = T / (kWaves * 2 * kTile) > 0 ? T / (kWaves * 2 * kTile) : 1;
     if (s > cap) s = cap;
     if (s > kMaxSplits) s = kMaxSplits;
     return (int)(s < 1 ? 1 : s);
 }
 
-int resolve_splits(int B, int H, int T, int splits) {
+// per_cu: workgroups of the kernel instance resident per CU (automatic splits
+// fill every CU that many times over).
+int resolve_splits(int B, int H, int T, int splits, int per_cu) {
     if (splits > 0) {
         int s = splits < T ? splits : T;
         return s < kMaxSplits ? s : kMaxSplits;
     }
-    return auto_splits(B, H, T);
+    return auto_splits(B, H, T, per_cu);
 }
 
 int64_t workspace_for(int B, int Hq, int S) {
@@ -1434,49 +1441,86 @@ int stage_bytes_rt(int f, int pb) {
     }
 }
 
-template <int G, int KF, int VF, bool TAB>
-int launch_gt(dim3 grid, size_t shm, hipStream_t st, const DParams& p) {
-    if (shm > 65536 &&
-        hipFuncSetAttribute((const void*)decode_partial_kernel<G, KF, VF, TAB>,
-                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm) != hipSuccess)
-        return reskv_host::check_launch("decode LDS attribute");
-    hipLaunchKernelGGL((decode_partial_kernel<G, KF, VF, TAB>), grid, dim3(kThreads), shm, st, p);
-    return reskv_host::check_launch("decode_partial_kernel");
-}
-
+// The partial kernel instance for (K format, V format, GQA ratio, RoPE table).
 template <int G, int KF, int VF>
-int launch_g(dim3 grid, size_t shm, hipStream_t st, const DParams& p) {
-    return p.rope ? launch_gt<G, KF, VF, true>(grid, shm, st, p) : launch_gt<G, KF, VF, false>(grid, shm, st, p);
+const void* kernel_g(bool tab) {
+    return tab ? reinterpret_cast<const void*>(&decode_partial_kernel<G, KF, VF, true>)
+               : reinterpret_cast<const void*>(&decode_partial_kernel<G, KF, VF, false>);
 }
 
 template <int KF, int VF>
-int launch_fmt(int G, dim3 grid, size_t shm, hipStream_t st, const DParams& p) {
+const void* kernel_fmt(int G, bool tab) {
     switch (G) {
-    case 1: return launch_g<1, KF, VF>(grid, shm, st, p);
-    case 2: return launch_g<2, KF, VF>(grid, shm, st, p);
-    case 4: return launch_g<4, KF, VF>(grid, shm, st, p);
-    default: return launch_g<8, KF, VF>(grid, shm, st, p);
+    case 1: return kernel_g<1, KF, VF>(tab);
+    case 2: return kernel_g<2, KF, VF>(tab);
+    case 4: return kernel_g<4, KF, VF>(tab);
+    default: return kernel_g<8, KF, VF>(tab);
     }
 }
 
-int launch_partial(int kf, int vf, int G, dim3 grid, size_t shm, hipStream_t st, const DParams& p) {
+const void* partial_kernel(int kf, int vf, int G, bool tab) {
     if (kf == vf) {
         switch (kf) {
-        case D_BITMAP: return launch_fmt<D_BITMAP, D_BITMAP>(G, grid, shm, st, p);
-        case D_TILED: return launch_fmt<D_TILED, D_TILED>(G, grid, shm, st, p);
-        case D_STRUCT16: return launch_fmt<D_STRUCT16, D_STRUCT16>(G, grid, shm, st, p);
-        case D_SINT4: return launch_fmt<D_SINT4, D_SINT4>(G, grid, shm, st, p);
-        case D_Q4: return launch_fmt<D_Q4, D_Q4>(G, grid, shm, st, p);
-        case D_Q2: return launch_fmt<D_Q2, D_Q2>(G, grid, shm, st, p);
-        case D_BITMAP_W: return launch_fmt<D_BITMAP_W, D_BITMAP_W>(G, grid, shm, st, p);
-        case D_TILED_W: return launch_fmt<D_TILED_W, D_TILED_W>(G, grid, shm, st, p);
-        default: return launch_fmt<D_DENSE, D_DENSE>(G, grid, shm, st, p);
+        case D_BITMAP: return kernel_fmt<D_BITMAP, D_BITMAP>(G, tab);
+        case D_TILED: return kernel_fmt<D_TILED, D_TILED>(G, tab);
+        case D_STRUCT16: return kernel_fmt<D_STRUCT16, D_STRUCT16>(G, tab);
+        case D_SINT4: return kernel_fmt<D_SINT4, D_SINT4>(G, tab);
+        case D_Q4: return kernel_fmt<D_Q4, D_Q4>(G, tab);
+        case D_Q2: return kernel_fmt<D_Q2, D_Q2>(G, tab);
+        case D_BITMAP_W: return kernel_fmt<D_BITMAP_W, D_BITMAP_W>(G, tab);
+        case D_TILED_W: return kernel_fmt<D_TILED_W, D_TILED_W>(G, tab);
+        default: return kernel_fmt<D_DENSE, D_DENSE>(G, tab);
         }
     }
-    if (kf == D_Q4 && vf == D_Q2) return launch_fmt<D_Q4, D_Q2>(G, grid, shm, st, p);
-    if (kf == D_Q2 && vf == D_Q4) return launch_fmt<D_Q2, D_Q4>(G, grid, shm, st, p);
-    RESKV_REQUIRE(false, "K and V residual formats must match (INT4/INT2 may mix)");
-    return 1;
+    if (kf == D_Q4 && vf == D_Q2) return kernel_fmt<D_Q4, D_Q2>(G, tab);
+    if (kf == D_Q2 && vf == D_Q4) return kernel_fmt<D_Q2, D_Q4>(G, tab);
+    return nullptr;
+}
+
+// LDS layout of one partial workgroup: centroid table (or the cross-wave merge
+// records, whichever is larger), permute tables, per-wave weight and V tiles,
+// per-wave K and V stages.
+struct PartialLds {
+    int lut_off, p_off, stage_off, stage_k, stage_v;
+    size_t bytes;
+};
+PartialLds partial_lds(int kf, const DTensor& k, int vf, const DTensor& v, int G) {
+    PartialLds L;
+    L.stage_k = stage_bytes_rt(kf, k.pb);
+    L.stage_v = stage_bytes_rt(vf, v.pb);
+    const int merge_bytes = kWaves * G * kPartStride * 4;
+    const int cent_bytes = kf != D_DENSE ? k.nc * kCPitch * 2 : 0;
+    L.lut_off = cent_bytes > merge_bytes ? cent_bytes : merge_bytes;
+    L.p_off = L.lut_off + (kLutWords + kStructLutWords) * 4;
+    L.stage_off = L.p_off + kWaves * (kTile * G + kTile * kVPitch) * 2;
+    L.bytes = (size_t)L.stage_off + (size_t)kWaves * (L.stage_k + L.stage_v);
+    return L;
+}
+
+// Workgroups of a partial kernel instance that are resident on one CU at once
+// (its registers and LDS), capped at kMaxGroupsPerCU; sets the instance's LDS
+// limit first.  Returns 0 on a runtime error.
+int groups_per_cu(const void* fn, size_t shm) {
+    if (shm > 65536 &&
+        hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm) != hipSuccess)
+        return 0;
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, kThreads, shm) != hipSuccess || n < 1) return 0;
+    return n < kMaxGroupsPerCU ? n : kMaxGroupsPerCU;
+}
+
+// The split count a decode of these tensors makes (splits <= 0: automatic).
+int splits_for(int kf, const DTensor& k, int vf, const DTensor& v, int G, bool tab, int B, int H, int T,
+               int splits, int* out) {
+    const void* fn = partial_kernel(kf, vf, G, tab);
+    RESKV_REQUIRE(fn != nullptr, "K and V residual formats must match (INT4/INT2 may mix)");
+    int per_cu = kMaxGroupsPerCU;
+    if (splits <= 0) {
+        per_cu = groups_per_cu(fn, partial_lds(kf, k, vf, v, G).bytes);
+        if (per_cu == 0) return reskv_host::check_launch("decode occupancy query");
+    }
+    *out = resolve_splits(B, H, T, splits, per_cu);
+    return 0;
 }
 
 int run_decode(const void* q, int kf, const DTensor& k, int vf, const DTensor& v, const float* inv_freq,
@@ -1488,9 +1532,18 @@ int run_decode(const void* q, int kf, const DTensor& k, int vf, const DTensor& v
     RESKV_REQUIRE(Hq % H == 0, "query heads must be a multiple of KV heads");
     const int G = Hq / H;
     RESKV_REQUIRE(G == 1 || G == 2 || G == 4 || G == 8, "supported GQA ratios are 1, 2, 4 and 8");
-    const int S = resolve_splits(B, H, T, splits);
-    RESKV_REQUIRE(ws != nullptr && ws_bytes >= workspace_for(B, Hq, S), "decode workspace too small");
     RESKV_REQUIRE((((uintptr_t)inv_freq | (uintptr_t)q) & 15u) == 0, "q and inv_freq must be 16-byte aligned");
+    const void* fn = partial_kernel(kf, vf, G, rope != nullptr);
+    RESKV_REQUIRE(fn != nullptr, "K and V residual formats must match (INT4/INT2 may mix)");
+    // the smallest split count these sizes can take, checked before any runtime call
+    RESKV_REQUIRE(ws != nullptr && ws_bytes >= workspace_for(B, Hq, resolve_splits(B, H, T, splits, 1)),
+                  "decode workspace too small");
+    const PartialLds L = partial_lds(kf, k, vf, v, G);
+    RESKV_REQUIRE(L.bytes <= 160 * 1024, "decode LDS requirement %zu exceeds 160 KiB", L.bytes);
+    const int per_cu = groups_per_cu(fn, L.bytes);  // also sets the instance's LDS limit
+    if (per_cu == 0) return reskv_host::check_launch("decode occupancy query");
+    const int S = resolve_splits(B, H, T, splits, per_cu);
+    RESKV_REQUIRE(ws != nullptr && ws_bytes >= workspace_for(B, Hq, S), "decode workspace too small");
     DParams p{};
     p.q = (const uint16_t*)q;
     p.k = k;
@@ -1506,23 +1559,21 @@ int run_decode(const void* q, int kf, const DTensor& k, int vf, const DTensor& v
     p.splits = S;
     p.qscale = scaling * kLog2e;
     p.one = 1.0f;
-    p.stage_k = stage_bytes_rt(kf, k.pb);
-    p.stage_v = stage_bytes_rt(vf, v.pb);
+    p.stage_k = L.stage_k;
+    p.stage_v = L.stage_v;
+    p.lut_off = L.lut_off;
+    p.p_off = L.p_off;
+    p.stage_off = L.stage_off;
     const bool cent = kf != D_DENSE;
-    const int merge_bytes = kWaves * G * kPartStride * 4;
-    const int cent_bytes = cent ? k.nc * kCPitch * 2 : 0;
-    const int region0 = cent_bytes > merge_bytes ? cent_bytes : merge_bytes;
-    p.lut_off = region0;
-    p.p_off = p.lut_off + (kLutWords + kStructLutWords) * 4;
-    p.stage_off = p.p_off + kWaves * (kTile * G + kTile * kVPitch) * 2;
-    const size_t shm = (size_t)p.stage_off + (size_t)kWaves * (p.stage_k + p.stage_v);
-    RESKV_REQUIRE(shm <= 160 * 1024, "decode LDS requirement %zu exceeds 160 KiB", shm);
     p.pm = (float*)ws;
     p.pl = p.pm + (long)B * Hq * S;
     p.pd = p.pl + (long)B * Hq * S;
     p.pb = p.pd + (long)B * Hq * S * kDim;
     hipStream_t st = (hipStream_t)stream;
-    if (launch_partial(kf, vf, G, dim3(S, H, B), shm, st, p)) return 1;
+    void* args[] = {&p};
+    if (hipLaunchKernel(fn, dim3(S, H, B), dim3(kThreads), args, L.bytes, st) != hipSuccess)
+        return reskv_host::check_launch("decode_partial_kernel");
+    if (reskv_host::check_launch("decode_partial_kernel")) return 1;
     if (recent != nullptr) {
         hipLaunchKernelGGL(decode_merge_kernel<true>, dim3(B * Hq), dim3(kMergeThreads), 0, st, p.pm, p.pl, p.pd,
                            p.pb, cent ? v.cent : nullptr, v.nc, v.cs, Hq, H, S, (uint16_t*)out, nullptr, nullptr,
@@ -1539,13 +1590,20 @@ int run_decode(const void* q, int kf, const DTensor& k, int vf, const DTensor& v
 
 extern "C" int64_t reskv_decode_workspace_bytes(int B, int Hq, int H, int T, int splits) {
     if (B <= 0 || Hq <= 0 || H <= 0 || T <= 0) return 0;
-    return workspace_for(B, Hq, resolve_splits(B, H, T, splits));
+    return workspace_for(B, Hq, resolve_splits(B, H, T, splits, kMaxGroupsPerCU));
 }
 
-extern "C" int reskv_decode_splits(int B, int Hq, int H, int T, int splits) {
-    (void)Hq;
-    if (B <= 0 || H <= 0 || T <= 0) return 0;
-    return resolve_splits(B, H, T, splits);
+extern "C" int reskv_decode_splits(const reskv_ctensor* k, const reskv_ctensor* v, int rope_table, int B, int Hq,
+                                   int H, int T, int splits) {
+    if (check_ct(k, "K") || check_ct(v, "V")) return -1;
+    if (B <= 0 || H <= 0 || T <= 0 || Hq <= 0 || Hq % H != 0) {
+        reskv_host::set_error("batch, head and token counts must be positive, query heads a multiple of KV heads");
+        return -1;
+    }
+    const int kf = dfmt_of(k), vf = dfmt_of(v);
+    int s = 0;
+    if (splits_for(kf, to_dt(k, kf, T), vf, to_dt(v, vf, T), Hq / H, rope_table != 0, B, H, T, splits, &s)) return -1;
+    return s;
 }
 
 extern "C" int reskv_decode_rope(const void* q, const reskv_ctensor* k, const reskv_ctensor* v,

@@ -33,13 +33,13 @@ def test_library_exports_every_declared_symbol():
     for name in declared_functions():
         assert hasattr(lib, name), name
         assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
-    assert lib.reskv_abi_version() == _lib.ABI_VERSION == 5
+    assert lib.reskv_abi_version() == _lib.ABI_VERSION == 6
 
 
 def test_a_library_of_another_abi_version_is_refused(monkeypatch):
     monkeypatch.setattr(_lib, "_lib", None)
-    monkeypatch.setattr(_lib, "ABI_VERSION", 4)
-    with pytest.raises(RuntimeError, match="ABI version 5, this binding needs 4"):
+    monkeypatch.setattr(_lib, "ABI_VERSION", 5)
+    with pytest.raises(RuntimeError, match="ABI version 6, this binding needs 5"):
         _lib.lib()
     assert _lib._lib is None  # nothing half-loaded is kept
 
@@ -156,12 +156,20 @@ def test_decode_descriptor_checks():
 
 def test_split_and_workspace_sizing():
     lib = _lib.lib()
-    for b in (1, 4, 8, 16, 32):
-        s = lib.reskv_decode_splits(b, 32, 8, 8192, 0)
-        assert 1 <= s <= 256
-        assert lib.reskv_decode_workspace_bytes(b, 32, 8, 8192, 0) == b * 32 * s * (2 + 128 + 64) * 4
-    assert lib.reskv_decode_splits(1, 32, 8, 5, 20) == 5  # explicit split counts are capped at T
-    assert lib.reskv_decode_splits(1, 32, 8, 8192, 20) == 20
+    record = (2 + 128 + 64) * 4  # one split partial per query head: m, l, 128 sums, 64 cluster masses
+    # the workspace covers the largest automatic count: ceil(4 * 256 / (B * H)) workgroups per head,
+    # capped at T / 128 (two 16-token tiles per wave)
+    for b, s in ((1, 64), (4, 32), (8, 16), (16, 8), (32, 4)):
+        assert lib.reskv_decode_workspace_bytes(b, 32, 8, 8192, 0) == b * 32 * s * record
+    assert lib.reskv_decode_workspace_bytes(1, 32, 8, 256, 0) == 32 * 2 * record
+    assert lib.reskv_decode_workspace_bytes(1, 32, 8, 8192, 20) == 32 * 20 * record
+    # explicit split counts need no device: capped at T
+    p = ctypes.c_void_p(16)
+    good = _lib.CTensor(p, p, p, p, None, 32, _lib.FMT_BITMAP, 64, 16)
+    assert lib.reskv_decode_splits(ctypes.byref(good), ctypes.byref(good), 1, 1, 32, 8, 5, 20) == 5
+    assert lib.reskv_decode_splits(ctypes.byref(good), ctypes.byref(good), 1, 1, 32, 8, 8192, 20) == 20
+    assert lib.reskv_decode_splits(ctypes.byref(good), ctypes.byref(good), 1, 1, 30, 8, 8192, 20) == -1
+    assert "multiple" in lib.reskv_last_error().decode()
     assert lib.reskv_kmeans_workspace_bytes(16, 8192, 32) > 0
 
 
