@@ -1517,7 +1517,7 @@ int splits_for(int kf, const DTensor& k, int vf, const DTensor& v, int G, bool t
     int per_cu = kMaxGroupsPerCU;
     if (splits <= 0) {
         per_cu = groups_per_cu(fn, partial_lds(kf, k, vf, v, G).bytes);
-        if (per_cu == 0) return reskv_host::check_launch("decode occupancy query");
+        RESKV_REQUIRE(per_cu > 0, "decode occupancy query failed: %s", hipGetErrorString(hipGetLastError()));
     }
     *out = resolve_splits(B, H, T, splits, per_cu);
     return 0;
@@ -1541,7 +1541,7 @@ int run_decode(const void* q, int kf, const DTensor& k, int vf, const DTensor& v
     const PartialLds L = partial_lds(kf, k, vf, v, G);
     RESKV_REQUIRE(L.bytes <= 160 * 1024, "decode LDS requirement %zu exceeds 160 KiB", L.bytes);
     const int per_cu = groups_per_cu(fn, L.bytes);  // also sets the instance's LDS limit
-    if (per_cu == 0) return reskv_host::check_launch("decode occupancy query");
+    RESKV_REQUIRE(per_cu > 0, "decode occupancy query failed: %s", hipGetErrorString(hipGetLastError()));
     const int S = resolve_splits(B, H, T, splits, per_cu);
     RESKV_REQUIRE(ws != nullptr && ws_bytes >= workspace_for(B, Hq, S), "decode workspace too small");
     DParams p{};
