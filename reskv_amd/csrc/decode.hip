@@ -51,16 +51,21 @@ typedef float float4_t __attribute__((ext_vector_type(4)));
 typedef short short4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) short4_t lds_short4_t;
 
+// MB: metadata bytes per token; PQ: 16-byte payload pieces per lane and
+// tile; SC: per-token scale; CENT: centroid + residual; MD1: the tile's
+// 16-byte metadata rows prefetched as one dword per lane (all 64 lanes)
+// instead of one row per token lane (fewer registers; measured faster for
+// the 4:16 format only).
 template <int F> struct Traits;
-template <> struct Traits<D_BITMAP> { static constexpr int MB = 16, PQ = 2; static constexpr bool SC = false, CENT = true; };
-template <> struct Traits<D_TILED> { static constexpr int MB = 16, PQ = 2; static constexpr bool SC = false, CENT = true; };
-template <> struct Traits<D_BITMAP_W> { static constexpr int MB = 16, PQ = 4; static constexpr bool SC = false, CENT = true; };
-template <> struct Traits<D_TILED_W> { static constexpr int MB = 16, PQ = 4; static constexpr bool SC = false, CENT = true; };
-template <> struct Traits<D_STRUCT16> { static constexpr int MB = 16, PQ = 1; static constexpr bool SC = false, CENT = true; };
-template <> struct Traits<D_SINT4> { static constexpr int MB = 8, PQ = 1; static constexpr bool SC = true, CENT = true; };
-template <> struct Traits<D_Q4> { static constexpr int MB = 0, PQ = 1; static constexpr bool SC = true, CENT = true; };
-template <> struct Traits<D_Q2> { static constexpr int MB = 0, PQ = 1; static constexpr bool SC = true, CENT = true; };
-template <> struct Traits<D_DENSE> { static constexpr int MB = 0, PQ = 4; static constexpr bool SC = false, CENT = false; };
+template <> struct Traits<D_BITMAP> { static constexpr int MB = 16, PQ = 2; static constexpr bool SC = false, CENT = true, MD1 = false; };
+template <> struct Traits<D_TILED> { static constexpr int MB = 16, PQ = 2; static constexpr bool SC = false, CENT = true, MD1 = false; };
+template <> struct Traits<D_BITMAP_W> { static constexpr int MB = 16, PQ = 4; static constexpr bool SC = false, CENT = true, MD1 = false; };
+template <> struct Traits<D_TILED_W> { static constexpr int MB = 16, PQ = 4; static constexpr bool SC = false, CENT = true, MD1 = false; };
+template <> struct Traits<D_STRUCT16> { static constexpr int MB = 16, PQ = 1; static constexpr bool SC = false, CENT = true, MD1 = true; };
+template <> struct Traits<D_SINT4> { static constexpr int MB = 8, PQ = 1; static constexpr bool SC = true, CENT = true, MD1 = false; };
+template <> struct Traits<D_Q4> { static constexpr int MB = 0, PQ = 1; static constexpr bool SC = true, CENT = true, MD1 = false; };
+template <> struct Traits<D_Q2> { static constexpr int MB = 0, PQ = 1; static constexpr bool SC = true, CENT = true, MD1 = false; };
+template <> struct Traits<D_DENSE> { static constexpr int MB = 0, PQ = 4; static constexpr bool SC = false, CENT = false, MD1 = false; };
 
 struct DTensor {
     const uint16_t* cent;     // fp16 [BH, nc, 128] (null for dense)
@@ -125,6 +130,7 @@ template <int F>
 struct Prefetch {
     uint4 pay[Traits<F>::PQ];
     uint4 meta;
+    uint32_t meta1;  // MD1: dword `lane` of the tile's metadata rows
     int id;
     float sc;
 };
@@ -167,7 +173,9 @@ __device__ __forceinline__ void prefetch(const WaveSrc<F>& W, int pb, int off, i
         P.pay[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(W.pay, o, 0, 0));
     }
     const int tok = lane < kTile ? off + lane : -1;
-    if constexpr (Tr::MB == 16) {
+    if constexpr (Tr::MB == 16 && Tr::MD1) {
+        P.meta1 = __builtin_amdgcn_raw_buffer_load_b32(W.meta, off * 16 + 4 * lane, 0, 0);  // past the range: 0
+    } else if constexpr (Tr::MB == 16) {
         P.meta = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(W.meta, tok >= 0 ? tok * 16 : kOut, 0, 0));
     } else if constexpr (Tr::MB == 8) {
         const uint2 m = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(W.meta, tok >= 0 ? tok * 8 : kOut, 0, 0));
@@ -211,8 +219,9 @@ __device__ __forceinline__ void stage_store(const Prefetch<F>& P, uint8_t* st, i
     for (int i = 0; i < Tr::PQ; ++i)
         if (slot[i] >= 0) lds_st16(st + slot[i], P.pay[i]);
     uint8_t* meta = st + kTile * (pb + kRowPad);
+    if constexpr (Tr::MB == 16 && Tr::MD1) reinterpret_cast<uint32_t*>(meta)[lane] = P.meta1;
     if (lane < kTile) {
-        if constexpr (Tr::MB == 16) lds_st16(meta + 16 * lane, P.meta);
+        if constexpr (Tr::MB == 16 && !Tr::MD1) lds_st16(meta + 16 * lane, P.meta);
         if constexpr (Tr::MB == 8) reinterpret_cast<uint2*>(meta)[lane] = make_uint2(P.meta.x, P.meta.y);
         int* ids = reinterpret_cast<int*>(meta + kTile * Tr::MB);
         const int cid = P.id < 0 ? 0 : (P.id >= nc ? nc - 1 : P.id);  // compression.cu:83-84
@@ -1498,15 +1507,20 @@ PartialLds partial_lds(int kf, const DTensor& k, int vf, const DTensor& v, int G
 }
 
 // Workgroups of a partial kernel instance that are resident on one CU at once
-// (its registers and LDS), capped at kMaxGroupsPerCU; sets the instance's LDS
-// limit first.  Returns 0 on a runtime error.
-int groups_per_cu(const void* fn, size_t shm) {
+// (its registers and LDS), capped at kMaxGroupsPerCU, and at two for the
+// formats that decode runs from LDS windows (a third bitmap workgroup per CU
+// measured 2% slower: it adds LDS traffic where the quantised formats, which
+// gain 10-13% from it, have none); sets the instance's LDS limit first.
+// Returns 0 on a runtime error.
+int groups_per_cu(const void* fn, size_t shm, int kf) {
     if (shm > 65536 &&
         hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm) != hipSuccess)
         return 0;
     int n = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, kThreads, shm) != hipSuccess || n < 1) return 0;
-    return n < kMaxGroupsPerCU ? n : kMaxGroupsPerCU;
+    const bool windows = kf == D_BITMAP || kf == D_BITMAP_W || kf == D_TILED || kf == D_TILED_W;
+    const int cap = windows ? 2 : kMaxGroupsPerCU;
+    return n < cap ? n : cap;
 }
 
 // The split count a decode of these tensors makes (splits <= 0: automatic).
@@ -1516,7 +1530,7 @@ int splits_for(int kf, const DTensor& k, int vf, const DTensor& v, int G, bool t
     RESKV_REQUIRE(fn != nullptr, "K and V residual formats must match (INT4/INT2 may mix)");
     int per_cu = kMaxGroupsPerCU;
     if (splits <= 0) {
-        per_cu = groups_per_cu(fn, partial_lds(kf, k, vf, v, G).bytes);
+        per_cu = groups_per_cu(fn, partial_lds(kf, k, vf, v, G).bytes, kf);
         RESKV_REQUIRE(per_cu > 0, "decode occupancy query failed: %s", hipGetErrorString(hipGetLastError()));
     }
     *out = resolve_splits(B, H, T, splits, per_cu);
@@ -1540,7 +1554,7 @@ int run_decode(const void* q, int kf, const DTensor& k, int vf, const DTensor& v
                   "decode workspace too small");
     const PartialLds L = partial_lds(kf, k, vf, v, G);
     RESKV_REQUIRE(L.bytes <= 160 * 1024, "decode LDS requirement %zu exceeds 160 KiB", L.bytes);
-    const int per_cu = groups_per_cu(fn, L.bytes);  // also sets the instance's LDS limit
+    const int per_cu = groups_per_cu(fn, L.bytes, kf);  // also sets the instance's LDS limit
     RESKV_REQUIRE(per_cu > 0, "decode occupancy query failed: %s", hipGetErrorString(hipGetLastError()));
     const int S = resolve_splits(B, H, T, splits, per_cu);
     RESKV_REQUIRE(ws != nullptr && ws_bytes >= workspace_for(B, Hq, S), "decode workspace too small");
