@@ -652,8 +652,10 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
     const WaveSrc<VF> wv = wave_src<VF>(P.v, bh * P.v.ts + t0, t1 - t0);
     // Tiles are prefetched kDepth ahead into register buffers used in turn
     // (two for formats of at most one 16-byte piece per lane and tensor, whose
-    // short tiles would otherwise wait on the load latency; one otherwise).
-    constexpr int kDepth = (KT::PQ + VT::PQ <= 2 && G <= 4) ? 2 : 1;
+    // short tiles would otherwise wait on the load latency; one otherwise, and
+    // one for 4:16, whose single buffer brings it to 161 VGPRs and three
+    // workgroups per CU, 4-6% faster at B = 32).
+    constexpr int kDepth = (KT::PQ + VT::PQ <= 2 && G <= 4 && KF != D_STRUCT16) ? 2 : 1;
     Prefetch<KF> pk[kDepth];
     Prefetch<VF> pv[kDepth];
 #pragma unroll
@@ -1506,20 +1508,22 @@ PartialLds partial_lds(int kf, const DTensor& k, int vf, const DTensor& v, int G
     return L;
 }
 
-// Workgroups of a partial kernel instance that are resident on one CU at once
-// (its registers and LDS), capped at kMaxGroupsPerCU, and at two for the
-// formats that decode runs from LDS windows (a third bitmap workgroup per CU
-// measured 2% slower: it adds LDS traffic where the quantised formats, which
-// gain 10-13% from it, have none); sets the instance's LDS limit first.
+// Workgroups of a partial kernel instance to fill each CU with: the number
+// resident at once (its registers and LDS; the instance's LDS limit is set
+// first), capped at kMaxGroupsPerCU, at two for the formats that decode runs
+// from LDS windows (a third bitmap workgroup per CU measured 2% slower: it adds
+// LDS traffic where the quantised formats, which gain 10-13% from it, have
+// none), and at two for 4:16 below 33 (batch, head) rows (its one-deep
+// prefetch leaves short tiles waiting: 4.6% slower at B = 4 with three).
 // Returns 0 on a runtime error.
-int groups_per_cu(const void* fn, size_t shm, int kf) {
+int groups_per_cu(const void* fn, size_t shm, int kf, long heads) {
     if (shm > 65536 &&
         hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm) != hipSuccess)
         return 0;
     int n = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, kThreads, shm) != hipSuccess || n < 1) return 0;
     const bool windows = kf == D_BITMAP || kf == D_BITMAP_W || kf == D_TILED || kf == D_TILED_W;
-    const int cap = windows ? 2 : kMaxGroupsPerCU;
+    const int cap = windows || (kf == D_STRUCT16 && heads <= 32) ? 2 : kMaxGroupsPerCU;
     return n < cap ? n : cap;
 }
 
@@ -1530,7 +1534,7 @@ int splits_for(int kf, const DTensor& k, int vf, const DTensor& v, int G, bool t
     RESKV_REQUIRE(fn != nullptr, "K and V residual formats must match (INT4/INT2 may mix)");
     int per_cu = kMaxGroupsPerCU;
     if (splits <= 0) {
-        per_cu = groups_per_cu(fn, partial_lds(kf, k, vf, v, G).bytes, kf);
+        per_cu = groups_per_cu(fn, partial_lds(kf, k, vf, v, G).bytes, kf, (long)B * H);
         RESKV_REQUIRE(per_cu > 0, "decode occupancy query failed: %s", hipGetErrorString(hipGetLastError()));
     }
     *out = resolve_splits(B, H, T, splits, per_cu);
@@ -1554,7 +1558,7 @@ int run_decode(const void* q, int kf, const DTensor& k, int vf, const DTensor& v
                   "decode workspace too small");
     const PartialLds L = partial_lds(kf, k, vf, v, G);
     RESKV_REQUIRE(L.bytes <= 160 * 1024, "decode LDS requirement %zu exceeds 160 KiB", L.bytes);
-    const int per_cu = groups_per_cu(fn, L.bytes, kf);  // also sets the instance's LDS limit
+    const int per_cu = groups_per_cu(fn, L.bytes, kf, (long)B * H);  // also sets the instance's LDS limit
     RESKV_REQUIRE(per_cu > 0, "decode occupancy query failed: %s", hipGetErrorString(hipGetLastError()));
     const int S = resolve_splits(B, H, T, splits, per_cu);
     RESKV_REQUIRE(ws != nullptr && ws_bytes >= workspace_for(B, Hq, S), "decode workspace too small");
