@@ -31,7 +31,7 @@ extern "C" {
 const char* reskv_last_error(void);
 
 /* Library ABI version (bumped on any signature, struct or data-layout
- * change, or when entry points are added); 6. */
+ * change, or when entry points are added, here or in reskv_llama.h); 7. */
 int reskv_abi_version(void);
 
 /* ------------------------------------------------------------------ *

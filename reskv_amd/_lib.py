@@ -14,7 +14,7 @@ LIB_PATH = _HERE / "libreskv_hip.so"
 _vp, _i, _i64, _f = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float
 
 # reskv_abi_version() of the library these signatures describe
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 
 class CTensor(ctypes.Structure):
@@ -67,6 +67,10 @@ SIGNATURES = {
     "reskv_merge_recent_qk": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _f, _vp, _vp]),
     "reskv_decode_dense": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _f, _i, _vp, _vp, _vp, _vp, _i64,
                                 _vp]),
+    # include/reskv_llama.h: fused steps of the end-to-end decode harness
+    "reskv_llama_rmsnorm": (_i, [_vp, _vp, _vp, _i, _i, _f, _vp]),
+    "reskv_llama_silu_mul": (_i, [_vp, _vp, _i, _i, _vp]),
+    "reskv_llama_qkv_rope": (_i, [_vp] * 4 + [_i, _i, _i] + [_vp] * 9 + [_i64, _i64, _i64, _vp]),
 }
 
 _lock = threading.Lock()

@@ -15,7 +15,7 @@ from pathlib import Path
 HERE = Path(__file__).resolve().parent
 CSRC = HERE / "csrc"
 LIB_NAME = "libreskv_hip.so"
-SOURCES = ("capi.hip", "encode.hip", "kmeans.hip", "decode.hip")
+SOURCES = ("capi.hip", "encode.hip", "kmeans.hip", "decode.hip", "llama_ops.hip")
 
 
 def library_path() -> Path:

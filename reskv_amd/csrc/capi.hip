@@ -32,4 +32,4 @@ int check_launch(const char* what) {
 
 extern "C" const char* reskv_last_error(void) { return g_error; }
 
-extern "C" int reskv_abi_version(void) { return 6; }
+extern "C" int reskv_abi_version(void) { return 7; }

@@ -17,8 +17,12 @@ RMSNorm gains).  Around attention the work has fixed shapes -- RMSNorm, the
 fused QKV projection and RoPE of the new token, the output projection and the
 gated MLP, the LM head with greedy argmax and the next token's embedding --
 and runs as HIP graphs, one before and one after each layer's attention.
-Attention and the cache bookkeeping, whose sizes change from step to step,
-run eagerly through the library.
+Inside them the RMSNorms, the split / rotation / append of the new token's
+Q, K and V, and the gated activation are single fused launches
+(``include/reskv_llama.h``), and the residual adds ride in the projection
+GEMMs (``addmm_``), so a layer's graphs hold eight kernels instead of about
+fifty.  Attention and the cache bookkeeping, whose sizes change from step to
+step, run eagerly through the library.
 """
 
 import math
@@ -27,6 +31,7 @@ from dataclasses import dataclass
 import torch
 import torch.nn.functional as F
 
+from . import _lib
 from ._extension import dense_decode
 from .cache import ResKVLayerCache
 from .config import ResKVKernelConfig
@@ -68,6 +73,46 @@ def llama3_inv_freq(shape: LlamaShape) -> torch.Tensor:
 def _rmsnorm(x, w, eps):
     xf = x.float()
     return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps) * w).to(x.dtype)
+
+
+def _stream(t):
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def fused_rmsnorm(x, w, eps, out):
+    """``_rmsnorm`` of fp16 rows x [R, hidden] into out, one launch."""
+    _lib.check(_lib.lib().reskv_llama_rmsnorm(x.data_ptr(), w.data_ptr(), out.data_ptr(), x.shape[0], x.shape[1],
+                                              eps, _stream(x)), "reskv_llama_rmsnorm")
+    return out
+
+
+def fused_silu_mul(gu, out):
+    """``silu(gu[:, :F]) * gu[:, F:]`` (fp16, as torch rounds it) into out [R, F], one launch."""
+    _lib.check(_lib.lib().reskv_llama_silu_mul(gu.data_ptr(), out.data_ptr(), gu.shape[0], out.shape[1],
+                                               _stream(gu)), "reskv_llama_silu_mul")
+    return out
+
+
+def fused_qkv_rope(qkv, cos, sin, pos, q, qr, k, kr, v, targets=None):
+    """Splits qkv [B, (Hq + 2 Hk) * 128] into q, k, v, writes ``_rotate`` of q and k
+    at position ``pos[0]`` (device) into qr, kr and, with ``targets = (rot, raw,
+    v_cache, slot)`` ([B, Hk, cap, 128] tensors, any of the three None; slot a
+    device int64), appends kr, k and v at token ``slot[0]``, one launch."""
+    b, hq, hk = q.shape[0], q.shape[1], k.shape[1]
+    rot = raw = vc = slot = None
+    strides = (0, 0, 0)
+    if targets is not None:
+        rot, raw, vc, slot = targets
+        ref = next(t for t in (rot, raw, vc) if t is not None)
+        for t in (rot, raw, vc):
+            if t is not None and (t.stride() != ref.stride() or t.stride(3) != 1 or t.shape[:2] != (b, hk)):
+                raise ValueError("cache append targets must share one [B, Hk, cap, 128] layout")
+        strides = ref.stride()[:3]
+    ptr = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+    _lib.check(_lib.lib().reskv_llama_qkv_rope(
+        qkv.data_ptr(), cos.data_ptr(), sin.data_ptr(), pos.data_ptr(), b, hq, hk, q.data_ptr(), qr.data_ptr(),
+        k.data_ptr(), kr.data_ptr(), v.data_ptr(), ptr(rot), ptr(raw), ptr(vc), ptr(slot), *strides,
+        _stream(qkv)), "reskv_llama_qkv_rope")
 
 
 def _rotate(x, cos, sin):
@@ -189,6 +234,8 @@ class GreedyDecoder:
         self.kr = torch.zeros_like(self.k)
         self.v = torch.zeros_like(self.k)
         self.attn = torch.zeros(batch, s.heads, s.head_dim, **f16)
+        self.h = torch.zeros(batch, s.hidden, **f16)  # RMSNorm output
+        self.act = torch.zeros(batch, s.ffn, **f16)  # gated activation
         self.tok = torch.zeros(batch, dtype=torch.int64, device=dev)
         self.pos_buf = torch.zeros(1, dtype=torch.int64, device=dev)
         self.slot_buf = torch.zeros(1, dtype=torch.int64, device=dev)  # ring slot of the new token
@@ -218,28 +265,19 @@ class GreedyDecoder:
     # -- fixed-shape parts as graphs -----------------------------------------
     def _pre(self, li, p):
         s = self.model.shape
-        h = _rmsnorm(self.x, p["n1"], s.rms_eps)
-        q, k, v = self._split_step(F.linear(h, p["wqkv"]))
-        cos = self.cos.index_select(0, self.pos_buf)
-        sin = self.sin.index_select(0, self.pos_buf)
-        self.q.copy_(q)
-        self.k.copy_(k)
-        self.v.copy_(v)
-        self.qr.copy_(_rotate(q, cos, sin))
-        self.kr.copy_(_rotate(k, cos, sin))
-        self._append(li)
+        fused_rmsnorm(self.x, p["n1"], s.rms_eps, self.h)
+        qkv = F.linear(self.h, p["wqkv"])
+        fused_qkv_rope(qkv, self.cos, self.sin, self.pos_buf, self.q, self.qr, self.k, self.kr, self.v,
+                       self._append_targets(li))
 
-    def _append(self, li):
-        """The new token's K/V into layer li's cache, at a slot read from device
-        memory (inside the pre graph, so the append costs no launches of its own)."""
+    def _append_targets(self, li):
+        """Where the pre graph appends the new token's K/V in layer li's cache: ring
+        slot ``live`` (ResKV: rotated K, pre-RoPE K, V) or position ``pos`` (dense:
+        pre-RoPE K, V), read from device memory when the graph runs."""
         if self.mode == "reskv":
             layer = self.caches[li]
-            layer.keys.index_copy_(2, self.slot_buf, self.kr[:, :, None])
-            layer.raw_keys.index_copy_(2, self.slot_buf, self.k[:, :, None])
-            layer.values.index_copy_(2, self.slot_buf, self.v[:, :, None])
-        else:
-            self.kc[li].index_copy_(2, self.pos_buf, self.k[:, :, None])
-            self.vc[li].index_copy_(2, self.pos_buf, self.v[:, :, None])
+            return layer.keys, layer.raw_keys, layer.values, self.slot_buf
+        return None, self.kc[li], self.vc[li], self.pos_buf
 
     def _set_slots(self):
         """Device copies of this step's position and ring slot (the layers' rings fill in step)."""
@@ -247,20 +285,17 @@ class GreedyDecoder:
         if self.mode == "reskv":
             self.slot_buf.fill_(self.caches[0].live)
 
-    def _split_step(self, qkv):
-        return self.model._split(qkv)
-
     def _post(self, p):
         s = self.model.shape
-        self.x += F.linear(self.attn.view(self.batch, s.hidden), p["wo"])
-        h = _rmsnorm(self.x, p["n2"], s.rms_eps)
-        gu = F.linear(h, p["wgu"])
-        act = F.silu(gu[:, : s.ffn]) * gu[:, s.ffn:]
-        self.x += F.linear(act, p["wd"])
+        # residual adds in the GEMM epilogue: x = x + attn @ wo^T (one rounding)
+        self.x.addmm_(self.attn.view(self.batch, s.hidden), p["wo"].t())
+        fused_rmsnorm(self.x, p["n2"], s.rms_eps, self.h)
+        fused_silu_mul(F.linear(self.h, p["wgu"]), self.act)
+        self.x.addmm_(self.act, p["wd"].t())
 
     def _head(self):
         s = self.model.shape
-        logits = F.linear(_rmsnorm(self.x, self.model.norm, s.rms_eps), self.model.lm_head)
+        logits = F.linear(fused_rmsnorm(self.x, self.model.norm, s.rms_eps, self.h), self.model.lm_head)
         self.tok.copy_(torch.argmax(logits, dim=-1))
         self.x.copy_(self.model.embed.index_select(0, self.tok))
 

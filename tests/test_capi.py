@@ -9,16 +9,17 @@ import pytest
 
 from reskv_amd import _lib
 
-HEADER = Path(__file__).resolve().parents[1] / "include" / "reskv_hip.h"
+INCLUDE = Path(__file__).resolve().parents[1] / "include"
+HEADER = INCLUDE / "reskv_hip.h"
 
 
-def declared_functions():
-    text = HEADER.read_text()
+def declared_functions(headers=None):
+    text = "".join(h.read_text() for h in (headers or sorted(INCLUDE.glob("*.h"))))
     return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\**\s+\**(reskv_\w+)\s*\(", text, flags=re.M)))
 
 
 def test_header_declares_the_operator_surface():
-    names = declared_functions()
+    names = declared_functions([HEADER])
     for required in ("reskv_compress_fp16", "reskv_compress_bitmap", "reskv_compress_quantized",
                      "reskv_compress_structured_int4", "reskv_compress_fp16_kv", "reskv_compress_bitmap_kv",
                      "reskv_kmeans", "reskv_kmeans_assign", "reskv_kmeans_kv",
@@ -33,13 +34,13 @@ def test_library_exports_every_declared_symbol():
     for name in declared_functions():
         assert hasattr(lib, name), name
         assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
-    assert lib.reskv_abi_version() == _lib.ABI_VERSION == 6
+    assert lib.reskv_abi_version() == _lib.ABI_VERSION == 7
 
 
 def test_a_library_of_another_abi_version_is_refused(monkeypatch):
     monkeypatch.setattr(_lib, "_lib", None)
     monkeypatch.setattr(_lib, "ABI_VERSION", 5)
-    with pytest.raises(RuntimeError, match="ABI version 6, this binding needs 5"):
+    with pytest.raises(RuntimeError, match="ABI version 7, this binding needs 5"):
         _lib.lib()
     assert _lib._lib is None  # nothing half-loaded is kept
 
@@ -270,3 +271,23 @@ def test_noalloc_decode_rejects_sizes_beyond_its_scratch_before_any_device_call(
                                            None, None, None, 0, 0, None, None)
     assert status != 0 and "allocation-free" in L.reskv_last_error().decode()
     assert L.reskv_decode_workspace_bytes(32, 32, 8, 8192, 0) <= 8 << 20
+
+
+def test_harness_op_argument_checks():
+    """The end-to-end harness's fused steps (include/reskv_llama.h) reject bad
+    arguments before any launch."""
+    lib = _lib.lib()
+    a = ctypes.c_void_p(256)  # aligned placeholder address, never dereferenced
+    assert "null" in _err(lib.reskv_llama_rmsnorm(None, a, a, 16, 4096, 1e-5, None))
+    assert "multiple of 8" in _err(lib.reskv_llama_rmsnorm(a, a, a, 16, 4100, 1e-5, None))
+    assert "up to 8192" in _err(lib.reskv_llama_rmsnorm(a, a, a, 16, 8200, 1e-5, None))
+    assert "aligned" in _err(lib.reskv_llama_rmsnorm(ctypes.c_void_p(258), a, a, 16, 4096, 1e-5, None))
+    assert lib.reskv_llama_rmsnorm(a, a, a, 0, 4096, 1e-5, None) == 0  # no rows: no launch
+    assert "multiple of 8" in _err(lib.reskv_llama_silu_mul(a, a, 16, 12, None))
+    assert "negative" in _err(lib.reskv_llama_silu_mul(a, a, -1, 16, None))
+    args = [a, a, a, a, 2, 32, 8] + [a] * 5
+    assert "head counts" in _err(lib.reskv_llama_qkv_rope(a, a, a, a, 2, 32, 7, *[a] * 5, None, None, None, None,
+                                                          0, 0, 0, None))
+    assert "slot" in _err(lib.reskv_llama_qkv_rope(*args, a, None, None, None, 1, 1, 1, None))
+    assert "strides" in _err(lib.reskv_llama_qkv_rope(*args, None, a, a, a, 1, 0, 1, None))
+    assert "null" in _err(lib.reskv_llama_qkv_rope(None, *args[1:], None, None, None, None, 0, 0, 0, None))

@@ -14,8 +14,8 @@ class _EagerAppend(GreedyDecoder):
     """The harness with the K/V append outside the graphs, through the cache's own
     ``update`` (ResKV) or slice copies (dense), and the output copied."""
 
-    def _append(self, li):
-        pass
+    def _append_targets(self, li):
+        return None
 
     def _attend(self, li):
         if self.mode == "reskv":
