@@ -529,7 +529,21 @@ def _check_recent_inputs(comp_out, comp_m, comp_l, v_recent, nh_kv, nh):
     return b, int(v_recent.shape[2])
 
 
-def _make_cluster_mass():
+def _fixed_shift_stats(res):
+    """The fixed-shift softmax's statistics (cluster_mass.cu:660, 874-888,
+    1046-1067): the reference sums exp(score) with the shift held at 0, so it
+    returns m = 0 and l = sum exp(score).  The online sum gives the same
+    normaliser as l * exp(m), which overflows to inf exactly where the
+    reference's unshifted sum does (scores above about 88)."""
+    if len(res) == 3:
+        out, m, l = res
+        res = [out, torch.zeros_like(m), l * torch.exp(m)]
+    return res
+
+
+def _make_cluster_mass(plan=None):
+    fixed_shift = bool(plan is not None and plan.fixed_shift)
+
     def decode_fp16(Q, kc, ki, kp, kbitmap, vc, vi, vp, vbitmap, nh_kv, nh, start_pos, pos_q, rope_base,
                     scaling, return_stats, splits, inv_freq):
         """Deferred unstructured FP16 decode (reskv/csrc/cluster_mass.cu:1177-1296)."""
@@ -562,8 +576,10 @@ def _make_cluster_mass():
             kd = _ctensor(kc, ki, kqv, kmeta, ks, fmt, bits)
             vd = _ctensor(vc, vi, vqv, vmeta, vs, fmt, bits)
             keep = (kc, ki, kqv, kmeta, vc, vi, vqv, vmeta) + ((ks, vs) if int4 else ())
-            return _decode(Q, kd, vd, keep, nh_kv, nh, start_pos, pos_q, rope_base, scaling, splits, inv_freq,
-                           bool(return_stats))
+            res = _decode(Q, kd, vd, keep, nh_kv, nh, start_pos, pos_q, rope_base, scaling, splits, inv_freq,
+                          bool(return_stats))
+            # the reference compiles the fixed shift into its structured INT4 kernel only
+            return _fixed_shift_stats(res) if int4 and fixed_shift else res
 
         op.__doc__ = ("Deferred structured %s decode (reskv/csrc/cluster_mass.cu:1298-1459)."
                       % ("INT4" if int4 else "FP16"))
@@ -664,7 +680,7 @@ def load_extension(family: str, plan: KernelPlan | None = None, device_index: in
         return _make_compression()
     if family == "attention":
         return _make_attention(plan)
-    return _make_cluster_mass()
+    return _make_cluster_mass(plan)
 
 
 def dense_decode(q, k, v, inv_freq, *, position, start_position=0, scaling=None, splits=0, out=None):

@@ -291,3 +291,19 @@ def test_harness_op_argument_checks():
     assert "slot" in _err(lib.reskv_llama_qkv_rope(*args, a, None, None, None, 1, 1, 1, None))
     assert "strides" in _err(lib.reskv_llama_qkv_rope(*args, None, a, a, a, 1, 0, 1, None))
     assert "null" in _err(lib.reskv_llama_qkv_rope(None, *args[1:], None, None, None, None, 0, 0, 0, None))
+
+
+def test_fixed_shift_statistics_conversion():
+    """The fixed-shift plan reports m = 0 and l = sum exp(score): the online
+    (m, l) pair converted, overflowing to inf where the unshifted sum does."""
+    import torch
+
+    from reskv_amd._extension import _fixed_shift_stats
+
+    out = torch.zeros(3, 128)
+    m = torch.tensor([1.5, -20.0, 100.0])
+    l = torch.tensor([3.0, 1.0, 2.0])
+    o2, m2, l2 = _fixed_shift_stats([out, m, l])
+    assert o2 is out and torch.equal(m2, torch.zeros(3))
+    assert torch.allclose(l2[:2], l[:2] * torch.exp(m[:2])) and torch.isinf(l2[2])
+    assert _fixed_shift_stats([out]) == [out]  # without statistics nothing changes

@@ -258,6 +258,36 @@ def test_split_count_invariance_and_stats(device, layout, sparsity):
         assert np.allclose(l_, el.reshape(-1), rtol=2e-4)
 
 
+def test_fixed_shift_plan_returns_the_unshifted_statistics(device):
+    """Structured INT4 under the fixed-shift plan (cluster_mass.cu:660, 874-888,
+    1046-1067): the same output as the online plan, m = 0 and l = sum exp(score)."""
+    from reskv_amd._extension import load_extension
+
+    k, v, q = outlier_kv(2, 2, 700, seed=12, gqa=4)
+    qf = q.reshape(-1, 128).contiguous()
+    freq = theta_freq()
+    args = (2, 8, 0, 800, 500000.0, 128 ** -0.5, True, 0, freq)
+    res = {}
+    for mode in ("online", "fixed_shift"):
+        cfg = ResKVKernelConfig(sparsity=0.75, bits=4, layout="structured", centroid_fusion="deferred",
+                                num_clusters=16, softmax_mode=mode)
+        cache = compress(k, v, cfg)
+        assert cache.key.plan.fixed_shift == (mode == "fixed_shift")
+        ext = load_extension("cluster_mass", cache.key.plan)
+        kc, ki, kp, km, ks = cache.key._native
+        vc, vi, vp, vm, vs = cache.value._native
+        res[mode] = [np_(t).astype(np.float64) for t in
+                     ext.decode_structured_int4(qf, kc, ki, kp, km, ks, vc, vi, vp, vm, vs, *args)]
+    eo, em, el = o.compressed_stats(np_(q).astype(np.float64), _dense(cache.key), _dense(cache.value),
+                                    position=800, freq=np_(freq))
+    (o_on, m_on, l_on), (o_fs, m_fs, l_fs) = res["online"], res["fixed_shift"]
+    assert np.array_equal(o_on, o_fs)
+    assert np.abs(o_fs - eo.reshape(-1, 128)).max() <= ATOL
+    assert (m_fs == 0).all()
+    assert np.allclose(l_fs, (el * np.exp(em)).reshape(-1), rtol=5e-4)
+    assert np.allclose(m_on, em.reshape(-1), atol=1e-3, rtol=1e-4)
+
+
 def _dense(ct):
     from tests.gpu_helpers import dense
 
