@@ -519,23 +519,29 @@ def copy_bandwidth(torch, device, nbytes=1 << 30, reps=10):
     return 2.0 * nbytes * reps / secs / 1e9
 
 
-def measured_traffic(b, t, sparsity, layout):
-    """HBM bytes per launch of the partial kernel from the committed rocprof run, if it is this workload.
+def measured_traffic(b, t, sparsity, layout, splits):
+    """(HBM bytes per launch of the partial kernel, where that figure comes from)
+    from the committed rocprof run if it is this workload, else (None, None).
 
     The figure comes from two rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE),
     each scaled by what the same counter reads for a device copy of known
     size; profiles/decode_partial_b32_s50.md holds the runs and the commands.
+    It is not measured by this run: the source names the profile, the split
+    count it was measured at and whether that is this run's split count.
     """
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "decode_traffic.json")
     try:
         with open(path) as f:
             rec = json.load(f)
     except (OSError, ValueError):
-        return None
+        return None, None
     w = rec.get("workload", {})
     if (w.get("batch"), w.get("seq_len"), w.get("sparsity"), w.get("layout")) != (b, t, sparsity, layout):
-        return None
-    return (rec["fetch_bytes"] + rec["write_bytes"]) * 1000
+        return None, None
+    source = {"profile": rec.get("source"), "file": "profiles/decode_traffic.json",
+              "measured_at_splits": w.get("splits"), "this_run_splits": splits,
+              "note": "copied from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE passes, not measured by this run"}
+    return (rec["fetch_bytes"] + rec["write_bytes"]) * 1000, source
 
 
 def main():
@@ -603,7 +609,7 @@ def main():
         print(json.dumps({"e2e": e2e}), flush=True)
     copy_gbps = copy_bandwidth(torch, device)
     cpu = None if args.no_cpu_baseline else cpu_baseline()
-    traffic = measured_traffic(args.batch, args.seq_len, args.sparsity, r["layout"])
+    traffic, traffic_source = measured_traffic(args.batch, args.seq_len, args.sparsity, r["layout"], r["splits"])
     secs = r["seconds"]
     line = {
         "metric": METRIC,
@@ -643,7 +649,7 @@ def main():
         },
         "roofline": {
             "bound": "hbm", "achieved": r["achieved_GBps"], "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-            "frac": r["frac"], "traffic": traffic,
+            "frac": r["frac"], "traffic": traffic, "traffic_source": traffic_source,
             "kernel": "one decode-attention call (decode_partial_kernel + decode_merge_kernel)",
             "bytes_per_call": r["bytes_per_call"],
             "copy_GBps": copy_gbps, "frac_of_copy": r["achieved_GBps"] / copy_gbps,

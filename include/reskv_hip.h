@@ -209,7 +209,8 @@ int reskv_rope_table(const float* inv_freq, int count, float* table, void* strea
 /* Joint softmax of the compressed result with precomputed fp32 recent scores.
  * Replaces the deferred ext.merge_recent (reskv/csrc/cluster_mass.cu:1461-1508,
  * op at :1515).  comp_out fp16 [B*Hq,128]; comp_m, comp_l fp32 [B*Hq];
- * scores fp32 [B,Hq,Tr]; v_recent fp16 [B,H,Tr,128]; out fp16 [B*Hq,128]. */
+ * scores fp32 [B,Hq,Tr]; v_recent fp16 [B,H,Tr,128], 16-byte aligned; out
+ * fp16 [B*Hq,128]. */
 int reskv_merge_recent_scores(const void* comp_out, const float* comp_m, const float* comp_l,
                               const float* scores, const void* v_recent, int B, int Hq,
                               int H, int Tr, void* out, void* stream);
@@ -218,7 +219,7 @@ int reskv_merge_recent_scores(const void* comp_out, const float* comp_m, const f
  * Replaces the per-token ext.merge_recent (reskv/csrc/attention.cu:839-906,
  * op at :1355).  q_rope fp16 [B*Hq,128]; k_recent, v_recent fp16 [B,H,*,128]:
  * the first Tr tokens of rows of r_stride tokens (r_stride<=0: Tr), so that a
- * ring buffer is read in place. */
+ * ring buffer is read in place; k_recent and v_recent 16-byte aligned. */
 int reskv_merge_recent_qk(const void* comp_out, const float* comp_m, const float* comp_l,
                           const void* q_rope, const void* k_recent, const void* v_recent,
                           int B, int Hq, int H, int Tr, int r_stride, float scaling, void* out,
@@ -248,9 +249,11 @@ int reskv_decode_recent(const void* q, const reskv_ctensor* k, const reskv_ctens
  * (hipGetSymbolAddress) on the first call.  Sizes whose partials exceed it
  * (reskv_decode_workspace_bytes(B, Hq, H, T, splits) > 8 MiB; the automatic
  * split count stays below that up to B*Hq = 10,000 rows) are rejected with an
- * error.  Every call on a GPU shares that GPU's array: calls that overlap on
- * one GPU race.  Arguments and result are those of reskv_decode_recent
- * (Tr = 0: plain decode). */
+ * error.  The array used is the current device's: `stream` must belong to
+ * the current device (the null stream does), otherwise the call is rejected.
+ * Every call on a GPU shares that GPU's array: calls that overlap on one GPU
+ * race.  Arguments and result are those of reskv_decode_recent (Tr = 0:
+ * plain decode). */
 int reskv_decode_recent_noalloc(const void* q, const reskv_ctensor* k, const reskv_ctensor* v,
                                 const float* inv_freq, const float* rope_table, int B, int Hq, int H, int T,
                                 int start_pos, int pos_q, float scaling, int splits, const void* q_rope,

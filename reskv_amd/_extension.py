@@ -16,6 +16,7 @@ that device without synchronising.
 """
 
 import ctypes
+import weakref
 from functools import lru_cache
 from types import SimpleNamespace
 
@@ -75,55 +76,85 @@ def _workspace(nbytes, device):
     return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
 
 
-# RoPE tables, one per frequency set: the caller's inv_freq tensor (keyed by
-# its storage address and version, the tensor itself held so that the address
-# cannot be reused) or the theta-derived set (keyed by theta).  Compressed
-# tokens keep their positions, so one table serves every layer and decode
-# step.  Tables are never freed: a table that grows is replaced, and the
+# RoPE tables, one per frequency set, keyed by the 64 fp32 frequency values
+# (content), or by theta for the theta-derived set.  Compressed tokens keep
+# their positions, so one table serves every layer and decode step.
+#
+# A caller's inv_freq tensor is matched to its content key through
+# _BY_TENSOR (storage address, offset and dtype; the version counter detects
+# in-place updates), whose entry is dropped by a finalizer when that tensor is
+# collected, so a reused address never maps to
+# a stale key; a tensor not seen before costs one 256-byte device-to-host copy
+# of its values.  Fresh tensors with equal values (a per-call `.float()` of an
+# fp16 buffer, a `.to(device)` copy) therefore share one table.
+#
+# At most _MAX_FREQ_SETS frequency sets are kept (least recently used
+# evicted; an evicted table is released to torch's allocator, whose reuse is
+# ordered on the current stream).  A table that grows is replaced, and the
 # replaced one stays alive in _RETIRED, because a captured HIP graph or work
-# still queued on another stream may hold its address.  Growth is geometric
+# queued on another stream may still hold its address; growth is geometric
 # (powers of two), so the retired tables add at most the size of the live one.
-# For graph capture: make one eager call at the largest position first, so
-# that no table is allocated while capturing.
-_ROPE_TABLES = {}
+# Graph capture: make one eager call with the same inv_freq tensor (or theta)
+# at the largest position first, so that nothing is copied or allocated while
+# capturing, and keep the captured sets within _MAX_FREQ_SETS.
+_MAX_FREQ_SETS = 8
+_ROPE_TABLES = {}  # content key -> (table fp32 [P, 128], frequencies fp32 [64]), in LRU order
+_BY_TENSOR = {}    # (device, storage address, offset, dtype) -> (version, content key)
 _RETIRED = []
 
 
-def _rope_table(freq, key, positions, source=None):
-    """fp32 [P, 128] table covering positions [0, positions), P a power of two."""
-    entry = _ROPE_TABLES.get(key)
-    if entry is not None and entry[0].shape[0] >= positions:
-        return entry[0]
-    count = 1 << max(10, (int(positions) - 1).bit_length())
+def _build_table(freq, count):
     table = torch.empty((count, 128), dtype=torch.float32, device=freq.device)
     with torch.cuda.device(freq.device):
         _lib.check(_lib.lib().reskv_rope_table(freq.data_ptr(), count, table.data_ptr(), _stream(freq.device)),
                    "rope_table")
-    if entry is not None:
-        _RETIRED.append(entry)
-    _ROPE_TABLES[key] = (table, source)
     return table
+
+
+def _table_for(key, freq, positions):
+    """(frequencies, fp32 [P, 128] table covering [0, positions)), P a power of two >= 1024."""
+    entry = _ROPE_TABLES.pop(key, None)
+    if entry is not None:
+        freq = entry[1]
+        if entry[0].shape[0] < positions:
+            _RETIRED.append(entry[0])
+            entry = None
+    if entry is None:
+        count = 1 << max(10, (int(positions) - 1).bit_length())
+        entry = (_build_table(freq, count), freq)
+    _ROPE_TABLES[key] = entry  # most recently used last
+    while len(_ROPE_TABLES) > _MAX_FREQ_SETS:
+        _ROPE_TABLES.pop(next(iter(_ROPE_TABLES)))
+    return entry[1], entry[0]
+
+
+def _content_key(inv_freq, dev):
+    ident = (dev, inv_freq.untyped_storage().data_ptr(), inv_freq.storage_offset(), inv_freq.dtype)
+    seen = _BY_TENSOR.get(ident)
+    if seen is not None and seen[0] == inv_freq._version:
+        return seen[1]
+    values = inv_freq.detach().reshape(64).to(device="cpu", dtype=torch.float32)
+    key = (dev, "freq", values.numpy().tobytes())
+    _BY_TENSOR[ident] = (inv_freq._version, key)  # an in-place update replaces the entry
+    if seen is None:
+        weakref.finalize(inv_freq, _BY_TENSOR.pop, ident, None)
+    return key
 
 
 def _rope(inv_freq, rope_base, dev, positions):
     """(fp32 frequencies, table) for the caller's inv_freq [64] (any float
-    dtype; the key is the caller's tensor, not a converted copy) or the
+    dtype, converted to fp32 as the reference's kernels read it) or the
     theta-derived set."""
     if inv_freq is not None and inv_freq.numel():
         _require(inv_freq.numel() == 64 and inv_freq.is_floating_point(), "inv_freq must be fp32 [64]")
-        key = (dev, inv_freq.untyped_storage().data_ptr(), inv_freq.storage_offset(), inv_freq._version)
-        entry = _ROPE_TABLES.get(key)
-        if entry is not None and entry[0].shape[0] >= positions:
-            return entry[1][1], entry[0]
-        freq = _frequencies(inv_freq.float(), rope_base, dev)
-        table = _rope_table(freq, key, positions, (inv_freq, freq))
-        return freq, table
+        key = _content_key(inv_freq, dev)
+        freq = None
+        if key not in _ROPE_TABLES:
+            freq = _frequencies(inv_freq.detach().reshape(64).float(), rope_base, dev)
+        return _table_for(key, freq, positions)
     key = (dev, "theta", float(rope_base))
-    entry = _ROPE_TABLES.get(key)
-    if entry is not None and entry[0].shape[0] >= positions:
-        return entry[1], entry[0]
-    freq = _frequencies(None, rope_base, dev)
-    return freq, _rope_table(freq, key, positions, freq)
+    freq = None if key in _ROPE_TABLES else _frequencies(None, rope_base, dev)
+    return _table_for(key, freq, positions)
 
 
 def _frequencies(inv_freq, rope_base, device):
@@ -533,8 +564,13 @@ def _fixed_shift_stats(res):
     """The fixed-shift softmax's statistics (cluster_mass.cu:660, 874-888,
     1046-1067): the reference sums exp(score) with the shift held at 0, so it
     returns m = 0 and l = sum exp(score).  The online sum gives the same
-    normaliser as l * exp(m), which overflows to inf exactly where the
-    reference's unshifted sum does (scores above about 88)."""
+    normaliser as l * exp(m), which overflows to inf where the reference's
+    unshifted sum does (scores above about 88).  The output is the online
+    one: where the reference's sums overflow, its output divides overflowed
+    sums (inf / inf = NaN, or 0 for a channel whose weighted sum stayed
+    finite), while this output stays the finite softmax average.  That
+    overflow case is parity unpinned; wherever the unshifted sums are finite
+    the outputs agree within the decode tolerance."""
     if len(res) == 3:
         out, m, l = res
         res = [out, torch.zeros_like(m), l * torch.exp(m)]

@@ -1652,7 +1652,8 @@ extern "C" int reskv_decode_recent(const void* q, const reskv_ctensor* k, const 
     const int rs = r_stride > 0 ? r_stride : Tr;
     RESKV_REQUIRE(rs >= Tr, "recent row stride shorter than the window");
     RESKV_REQUIRE(Tr == 0 || (q_rope && k_recent && v_recent), "null recent tensors");
-    RESKV_REQUIRE(Tr == 0 || ((((uintptr_t)k_recent) & 15u) == 0), "recent K must be 16-byte aligned");
+    RESKV_REQUIRE(Tr == 0 || ((((uintptr_t)k_recent | (uintptr_t)v_recent) & 15u) == 0),
+                  "recent K and V must be 16-byte aligned");
     const RecentArgs rc{(const uint16_t*)q_rope, (const uint16_t*)k_recent, (const uint16_t*)v_recent, Tr, rs, scaling};
     const int kf = dfmt_of(k), vf = dfmt_of(v);
     return run_decode(q, kf, to_dt(k, kf, T), vf, to_dt(v, vf, T), inv_freq, rope_table, B, Hq, H, T, start_pos,
@@ -1710,6 +1711,16 @@ extern "C" int reskv_decode_recent_noalloc(const void* q, const reskv_ctensor* k
                   "reskv_decode_recent_noalloc: these sizes need %lld bytes of split-K scratch; the "
                   "allocation-free entry point holds %lld (use reskv_decode_recent with a workspace)",
                   (long long)need, (long long)kNoAllocScratchBytes);
+    // the array used is the current device's: a stream of another device is rejected
+    // (the null stream is the current device's)
+    int cur = -1, sdev = -1;
+    RESKV_REQUIRE(hipGetDevice(&cur) == hipSuccess, "no current HIP device");
+    if (stream == nullptr) sdev = cur;
+    else RESKV_REQUIRE(hipStreamGetDevice((hipStream_t)stream, &sdev) == hipSuccess,
+                       "reskv_decode_recent_noalloc: cannot query the stream's device");
+    RESKV_REQUIRE(sdev == cur,
+                  "reskv_decode_recent_noalloc: the stream belongs to device %d but device %d is current; make "
+                  "the stream's device current (its scratch array is used)", sdev, cur);
     void* ws = scratch_on_current_device();
     if (ws == nullptr) return 1;
     return reskv_decode_recent(q, k, v, inv_freq, rope_table, B, Hq, H, T, start_pos, pos_q, scaling, splits,
@@ -1771,6 +1782,7 @@ extern "C" int reskv_merge_recent_scores(const void* comp_out, const float* comp
     RESKV_REQUIRE(comp_out && comp_m && comp_l && out, "null pointer argument");
     RESKV_REQUIRE(B > 0 && H > 0 && Hq % H == 0 && Tr >= 0, "bad recent-merge sizes");
     RESKV_REQUIRE(Tr == 0 || (scores && v_recent), "null recent scores/values");
+    RESKV_REQUIRE(Tr == 0 || (((uintptr_t)v_recent) & 15u) == 0, "recent V must be 16-byte aligned");
     hipLaunchKernelGGL(merge_recent_kernel, dim3(B * Hq), dim3(kMergeThreads), 0, (hipStream_t)stream,
                        (const uint16_t*)comp_out, comp_m, comp_l, scores, nullptr, nullptr,
                        (const uint16_t*)v_recent, Hq, H, Tr, Tr, 1.0f, (uint16_t*)out);
@@ -1786,7 +1798,8 @@ extern "C" int reskv_merge_recent_qk(const void* comp_out, const float* comp_m, 
     const int rs = r_stride > 0 ? r_stride : Tr;
     RESKV_REQUIRE(rs >= Tr, "recent row stride shorter than the window");
     RESKV_REQUIRE(Tr == 0 || (q_rope && k_recent && v_recent), "null recent tensors");
-    RESKV_REQUIRE(Tr == 0 || ((((uintptr_t)k_recent) & 15u) == 0), "recent K must be 16-byte aligned");
+    RESKV_REQUIRE(Tr == 0 || ((((uintptr_t)k_recent | (uintptr_t)v_recent) & 15u) == 0),
+                  "recent K and V must be 16-byte aligned");
     hipLaunchKernelGGL(merge_recent_kernel, dim3(B * Hq), dim3(kMergeThreads), 0, (hipStream_t)stream,
                        (const uint16_t*)comp_out, comp_m, comp_l, nullptr, (const uint16_t*)q_rope,
                        (const uint16_t*)k_recent, (const uint16_t*)v_recent, Hq, H, Tr, rs, scaling, (uint16_t*)out);

@@ -79,8 +79,35 @@ def _stream(t):
     return torch.cuda.current_stream(t.device).cuda_stream
 
 
+def _need(cond, msg):
+    if not cond:
+        raise ValueError(msg)
+
+
+def _fp16_rows(name, t, rows=None, width=None):
+    """t must be a contiguous fp16 CUDA matrix (of the given rows / width)."""
+    _need(t.dtype == torch.float16 and t.dim() == 2 and t.is_contiguous(), f"{name} must be a contiguous fp16 matrix")
+    _need(rows is None or t.shape[0] == rows, f"{name} has {t.shape[0]} rows, expected {rows}")
+    _need(width is None or t.shape[1] == width, f"{name} has {t.shape[1]} columns, expected {width}")
+
+
+def _fp16_heads(name, t, b, heads):
+    _need(t.dtype == torch.float16 and t.is_contiguous() and tuple(t.shape) == (b, heads, 128),
+          f"{name} must be a contiguous fp16 tensor [{b}, {heads}, 128]")
+
+
+def _on_gpu(*tensors):
+    """Checked last, after every shape, dtype and layout check."""
+    _need(all(t is None or t.is_cuda for t in tensors), "every tensor must be a CUDA tensor")
+
+
 def fused_rmsnorm(x, w, eps, out):
     """``_rmsnorm`` of fp16 rows x [R, hidden] into out, one launch."""
+    _fp16_rows("x", x)
+    _fp16_rows("out", out, x.shape[0], x.shape[1])
+    _need(w.dtype == torch.float16 and w.is_contiguous() and w.numel() == x.shape[1],
+          "w must be a contiguous fp16 vector of the hidden size")
+    _on_gpu(x, w, out)
     _lib.check(_lib.lib().reskv_llama_rmsnorm(x.data_ptr(), w.data_ptr(), out.data_ptr(), x.shape[0], x.shape[1],
                                               eps, _stream(x)), "reskv_llama_rmsnorm")
     return out
@@ -88,6 +115,9 @@ def fused_rmsnorm(x, w, eps, out):
 
 def fused_silu_mul(gu, out):
     """``silu(gu[:, :F]) * gu[:, F:]`` (fp16, as torch rounds it) into out [R, F], one launch."""
+    _fp16_rows("out", out)
+    _fp16_rows("gu", gu, out.shape[0], 2 * out.shape[1])
+    _on_gpu(gu, out)
     _lib.check(_lib.lib().reskv_llama_silu_mul(gu.data_ptr(), out.data_ptr(), gu.shape[0], out.shape[1],
                                                _stream(gu)), "reskv_llama_silu_mul")
     return out
@@ -98,16 +128,28 @@ def fused_qkv_rope(qkv, cos, sin, pos, q, qr, k, kr, v, targets=None):
     at position ``pos[0]`` (device) into qr, kr and, with ``targets = (rot, raw,
     v_cache, slot)`` ([B, Hk, cap, 128] tensors, any of the three None; slot a
     device int64), appends kr, k and v at token ``slot[0]``, one launch."""
+    _need(q.dim() == 3 and k.dim() == 3, "q must be [B, Hq, 128] and k [B, Hk, 128]")
     b, hq, hk = q.shape[0], q.shape[1], k.shape[1]
+    _fp16_rows("qkv", qkv, b, (hq + 2 * hk) * 128)
+    for name, t, heads in (("q", q, hq), ("qr", qr, hq), ("k", k, hk), ("kr", kr, hk), ("v", v, hk)):
+        _fp16_heads(name, t, b, heads)
+    _need(all(t.dtype == torch.float32 and t.dim() == 2 and t.shape[1] == 64 and t.is_contiguous()
+              for t in (cos, sin)) and cos.shape == sin.shape,
+          "cos and sin must be contiguous fp32 tables [P, 64] of one shape")
+    _need(pos.dtype == torch.int64 and pos.numel() >= 1, "pos must be an int64 tensor")
     rot = raw = vc = slot = None
     strides = (0, 0, 0)
     if targets is not None:
         rot, raw, vc, slot = targets
+        _need(slot is not None and slot.dtype == torch.int64 and slot.numel() >= 1, "slot must be an int64 tensor")
         ref = next(t for t in (rot, raw, vc) if t is not None)
         for t in (rot, raw, vc):
-            if t is not None and (t.stride() != ref.stride() or t.stride(3) != 1 or t.shape[:2] != (b, hk)):
+            if t is not None and (t.dtype != torch.float16 or t.dim() != 4 or t.shape[3] != 128
+                                  or t.stride() != ref.stride() or t.stride(3) != 1 or t.shape[:2] != (b, hk)):
                 raise ValueError("cache append targets must share one [B, Hk, cap, 128] layout")
         strides = ref.stride()[:3]
+
+    _on_gpu(qkv, cos, sin, pos, q, qr, k, kr, v, rot, raw, vc, slot)
     ptr = lambda t: None if t is None else t.data_ptr()  # noqa: E731
     _lib.check(_lib.lib().reskv_llama_qkv_rope(
         qkv.data_ptr(), cos.data_ptr(), sin.data_ptr(), pos.data_ptr(), b, hq, hk, q.data_ptr(), qr.data_ptr(),

@@ -307,3 +307,22 @@ def test_fixed_shift_statistics_conversion():
     assert o2 is out and torch.equal(m2, torch.zeros(3))
     assert torch.allclose(l2[:2], l[:2] * torch.exp(m[:2])) and torch.isinf(l2[2])
     assert _fixed_shift_stats([out]) == [out]  # without statistics nothing changes
+
+
+def test_misaligned_recent_values_are_rejected_before_any_launch():
+    """The recent join stages V rows with 16-byte loads: every entry point that
+    reads recent V refuses a pointer off a 16-byte boundary (an fp16 tensor at
+    an odd storage offset) on the host."""
+    lib = _lib.lib()
+    p = ctypes.c_void_p(16)
+    odd = ctypes.c_void_p(18)
+    assert "recent V must be 16-byte aligned" in _err(
+        lib.reskv_merge_recent_scores(p, p, p, p, odd, 1, 4, 1, 5, p, None))
+    assert "recent K and V must be 16-byte aligned" in _err(
+        lib.reskv_merge_recent_qk(p, p, p, p, p, odd, 1, 4, 1, 5, 0, 0.1, p, None))
+    assert "recent K and V must be 16-byte aligned" in _err(
+        lib.reskv_merge_recent_qk(p, p, p, p, odd, p, 1, 4, 1, 5, 0, 0.1, p, None))
+    good = _lib.CTensor(p, p, p, p, None, 32, _lib.FMT_BITMAP, 64, 16)
+    assert "recent K and V must be 16-byte aligned" in _err(
+        lib.reskv_decode_recent(p, ctypes.byref(good), ctypes.byref(good), p, None, 1, 4, 1, 16, 0, 15, 0.1, 0, p,
+                                p, odd, 5, 0, p, p, 1 << 30, None))

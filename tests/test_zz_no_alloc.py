@@ -66,7 +66,8 @@ def test_noalloc_rejects_sizes_beyond_its_scratch(device):
     kd, vd, keep = cache_descriptors(cache)
     f, table = _rope(freq, 500000.0, q.device, 256)
     L = _lib.lib()
-    # 1024 explicit splits (capped at T = 256): 8 * 256 * 776 B fits; B = 64 rows of 256 splits do not
+    # 256 explicit splits: B = 64 batch rows x 8 query heads x 256 splits x 776 B per split record
+    # (13 MB) exceed the 8 MiB array
     status = L.reskv_decode_recent_noalloc(q.data_ptr(), ctypes.byref(kd), ctypes.byref(vd), f.data_ptr(),
                                            table.data_ptr(), 64, 8, 2, 256, 0, pos, 0.1, 256, None, None, None, 0,
                                            0, None, None)
