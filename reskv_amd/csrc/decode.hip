@@ -51,21 +51,24 @@ typedef float float4_t __attribute__((ext_vector_type(4)));
 typedef short short4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) short4_t lds_short4_t;
 
-// MB: metadata bytes per token; PQ: 16-byte payload pieces per lane and
-// tile; SC: per-token scale; CENT: centroid + residual; MD1: the tile's
-// 16-byte metadata rows prefetched as one dword per lane (all 64 lanes)
-// instead of one row per token lane (fewer registers; measured faster for
-// the 4:16 format only).
+// MB: metadata bytes per token; PQ: 16-byte payload pieces per lane and tile
+// (the payload rows are staged in LDS, where the decoders gather from them);
+// DEPTH: tiles prefetched ahead (two where the registers allow it); SC:
+// per-token scale; CENT: centroid + residual.  Every lane loads its token's
+// metadata row, cluster id and scale itself, so they need no LDS round trip.
+// (Each lane loading only the payload bytes of its own channels straight into
+// registers, two to four narrow loads per tensor instead of one 16-byte load
+// per lane, measured 3-10% slower for INT2 and 4:16, equal for INT4.)
 template <int F> struct Traits;
-template <> struct Traits<D_BITMAP> { static constexpr int MB = 16, PQ = 2; static constexpr bool SC = false, CENT = true, MD1 = false; };
-template <> struct Traits<D_TILED> { static constexpr int MB = 16, PQ = 2; static constexpr bool SC = false, CENT = true, MD1 = false; };
-template <> struct Traits<D_BITMAP_W> { static constexpr int MB = 16, PQ = 4; static constexpr bool SC = false, CENT = true, MD1 = false; };
-template <> struct Traits<D_TILED_W> { static constexpr int MB = 16, PQ = 4; static constexpr bool SC = false, CENT = true, MD1 = false; };
-template <> struct Traits<D_STRUCT16> { static constexpr int MB = 16, PQ = 1; static constexpr bool SC = false, CENT = true, MD1 = true; };
-template <> struct Traits<D_SINT4> { static constexpr int MB = 8, PQ = 1; static constexpr bool SC = true, CENT = true, MD1 = false; };
-template <> struct Traits<D_Q4> { static constexpr int MB = 0, PQ = 1; static constexpr bool SC = true, CENT = true, MD1 = false; };
-template <> struct Traits<D_Q2> { static constexpr int MB = 0, PQ = 1; static constexpr bool SC = true, CENT = true, MD1 = false; };
-template <> struct Traits<D_DENSE> { static constexpr int MB = 0, PQ = 4; static constexpr bool SC = false, CENT = false, MD1 = false; };
+template <> struct Traits<D_BITMAP> { static constexpr int MB = 16, PQ = 2, DEPTH = 1; static constexpr bool SC = false, CENT = true; };
+template <> struct Traits<D_TILED> { static constexpr int MB = 16, PQ = 2, DEPTH = 1; static constexpr bool SC = false, CENT = true; };
+template <> struct Traits<D_BITMAP_W> { static constexpr int MB = 16, PQ = 4, DEPTH = 1; static constexpr bool SC = false, CENT = true; };
+template <> struct Traits<D_TILED_W> { static constexpr int MB = 16, PQ = 4, DEPTH = 1; static constexpr bool SC = false, CENT = true; };
+template <> struct Traits<D_STRUCT16> { static constexpr int MB = 16, PQ = 1, DEPTH = 1; static constexpr bool SC = false, CENT = true; };
+template <> struct Traits<D_SINT4> { static constexpr int MB = 8, PQ = 1, DEPTH = 2; static constexpr bool SC = true, CENT = true; };
+template <> struct Traits<D_Q4> { static constexpr int MB = 0, PQ = 1, DEPTH = 2; static constexpr bool SC = true, CENT = true; };
+template <> struct Traits<D_Q2> { static constexpr int MB = 0, PQ = 1, DEPTH = 2; static constexpr bool SC = true, CENT = true; };
+template <> struct Traits<D_DENSE> { static constexpr int MB = 0, PQ = 4, DEPTH = 1; static constexpr bool SC = false, CENT = false; };
 
 struct DTensor {
     const uint16_t* cent;     // fp16 [BH, nc, 128] (null for dense)
@@ -126,13 +129,17 @@ __device__ __forceinline__ void lds_st16(void* p, uint4 v) {
     q[1] = make_uint2(v.z, v.w);
 }
 
+__device__ __forceinline__ int clamp_id(int id, int nc) { return id < 0 ? 0 : (id >= nc ? nc - 1 : id); }
+
 template <int F>
 struct Prefetch {
-    uint4 pay[Traits<F>::PQ];
-    uint4 meta;
-    uint32_t meta1;  // MD1: dword `lane` of the tile's metadata rows
-    int id;
-    float sc;
+    uint4 pay[Traits<F>::PQ];  // payload pieces, staged into LDS
+    uint4 meta;  // this lane's token's metadata row (MB = 8: x, y)
+    // its cluster id and fp16 scale bits as loaded: kept in their stored
+    // widths and widened only where used, so that no conversion next to the
+    // load (or at the loop's back edge) makes the prefetch wait for itself
+    int8_t id;
+    uint16_t sc;
 };
 
 // The bytes of one wave's token range [t0, t1) of one tensor as raw buffer
@@ -160,47 +167,51 @@ __device__ __forceinline__ WaveSrc<F> wave_src(const DTensor& X, long row0, int 
     return w;
 }
 
-// Loads the raw bytes of the tile starting `off` tokens into the wave's range.
+__device__ __forceinline__ uint4 buf_b128(__amdgpu_buffer_rsrc_t r, int off) {
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+__device__ __forceinline__ uint2 buf_b64(__amdgpu_buffer_rsrc_t r, int off) {
+    return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
+}
+
+// Loads the tile starting `off` tokens into the wave's range: the payload rows
+// as 16-byte pieces q = lane + 64 i (bytes [16 (q % per_tok), +16) of row
+// q / per_tok), and in lane L = 16 g + t token t's metadata row, cluster id
+// and scale.
 template <int F>
 __device__ __forceinline__ void prefetch(const WaveSrc<F>& W, int pb, int off, int lane, Prefetch<F>& P) {
     using Tr = Traits<F>;
     constexpr int kOut = 0x7FFFFFF0;  // an offset past every range: the load returns zero
+    const int tok = off + (lane & 15);
     const int per_tok = pb >> 4;
 #pragma unroll
     for (int i = 0; i < Tr::PQ; ++i) {
         const int q = lane + kWave * i;
-        const int o = q < kTile * per_tok ? off * pb + 16 * q : kOut;
-        P.pay[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(W.pay, o, 0, 0));
+        P.pay[i] = buf_b128(W.pay, q < kTile * per_tok ? off * pb + 16 * q : kOut);
     }
-    const int tok = lane < kTile ? off + lane : -1;
-    if constexpr (Tr::MB == 16 && Tr::MD1) {
-        P.meta1 = __builtin_amdgcn_raw_buffer_load_b32(W.meta, off * 16 + 4 * lane, 0, 0);  // past the range: 0
-    } else if constexpr (Tr::MB == 16) {
-        P.meta = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(W.meta, tok >= 0 ? tok * 16 : kOut, 0, 0));
+    if constexpr (Tr::MB == 16) {
+        P.meta = buf_b128(W.meta, tok * 16);
     } else if constexpr (Tr::MB == 8) {
-        const uint2 m = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(W.meta, tok >= 0 ? tok * 8 : kOut, 0, 0));
+        const uint2 m = buf_b64(W.meta, tok * 8);
         P.meta = make_uint4(m.x, m.y, 0, 0);
     }
-    if constexpr (Tr::CENT)
-        P.id = (int)(int8_t)__builtin_amdgcn_raw_buffer_load_b8(W.ids, tok >= 0 ? tok : kOut, 0, 0);
-    if constexpr (Tr::SC)
-        P.sc = h2f(__builtin_amdgcn_raw_buffer_load_b16(W.scale, tok >= 0 ? tok * 2 : kOut, 0, 0));
+    if constexpr (Tr::CENT) P.id = (int8_t)__builtin_amdgcn_raw_buffer_load_b8(W.ids, tok, 0, 0);
+    if constexpr (Tr::SC) P.sc = __builtin_amdgcn_raw_buffer_load_b16(W.scale, tok * 2, 0, 0);
 }
 
-// Stage layout (bytes): payload [16][pb + kRowPad] | meta [16][MB] | ids int32[16] |
-// scale f32[16] | ids uint8[16].  Ids are stored clamped to [0, nc - 1]; the
-// byte copy feeds the one-hot operand of the cluster mass.  The 8-byte pad
-// staggers consecutive payload rows over the LDS banks (16 lanes read 16
+// Stage layout (bytes): payload [16][pb + kRowPad] | cluster ids uint8[16]
+// (clamped to [0, nc - 1]; the Value ids feed the one-hot operand of the
+// cluster mass).  The 8-byte row
+// pad staggers consecutive payload rows over the LDS banks (16 lanes read 16
 // different rows at similar offsets); rows are 8-byte aligned, so wide stage
 // accesses are done as 8-byte halves.
 template <int F>
 __host__ __device__ constexpr int stage_bytes(int pb) {
-    return kTile * (pb + kRowPad) + kTile * Traits<F>::MB + 2 * kTile * 4 + kTile;
+    return kTile * (pb + kRowPad) + kTile;
 }
 
-// LDS byte offsets of this lane's prefetch pieces inside the stage (piece
-// q = lane + 64 i is bytes [16 (q % per_tok), +16) of token row q / per_tok),
-// or -1 past the tile.  The same for every tile, so computed once.
+// LDS byte offsets of this lane's payload pieces inside the stage, or -1 past
+// the tile.  The same for every tile, so computed once.
 template <int F>
 __device__ __forceinline__ void stage_slots(int pb, int lane, int* slot) {
     const int per_tok = pb >> 4;
@@ -211,43 +222,47 @@ __device__ __forceinline__ void stage_slots(int pb, int lane, int* slot) {
     }
 }
 
-template <int F>
+// IDS: also store the tile's clamped cluster ids as bytes.
+template <int F, bool IDS>
 __device__ __forceinline__ void stage_store(const Prefetch<F>& P, uint8_t* st, int pb, const int* slot, int lane,
                                             int nc) {
     using Tr = Traits<F>;
 #pragma unroll
     for (int i = 0; i < Tr::PQ; ++i)
         if (slot[i] >= 0) lds_st16(st + slot[i], P.pay[i]);
-    uint8_t* meta = st + kTile * (pb + kRowPad);
-    if constexpr (Tr::MB == 16 && Tr::MD1) reinterpret_cast<uint32_t*>(meta)[lane] = P.meta1;
-    if (lane < kTile) {
-        if constexpr (Tr::MB == 16 && !Tr::MD1) lds_st16(meta + 16 * lane, P.meta);
-        if constexpr (Tr::MB == 8) reinterpret_cast<uint2*>(meta)[lane] = make_uint2(P.meta.x, P.meta.y);
-        int* ids = reinterpret_cast<int*>(meta + kTile * Tr::MB);
-        const int cid = P.id < 0 ? 0 : (P.id >= nc ? nc - 1 : P.id);  // compression.cu:83-84
-        ids[lane] = cid;
-        reinterpret_cast<float*>(ids + kTile)[lane] = P.sc;
-        reinterpret_cast<uint8_t*>(ids + 2 * kTile)[lane] = (uint8_t)cid;
+    if (IDS && Tr::CENT && lane < kTile) {
+        const int cid = clamp_id(P.id, nc);  // compression.cu:83-84
+        st[kTile * (pb + kRowPad) + lane] = (uint8_t)cid;
     }
 }
-
 
 template <int F>
 struct StageView {
     const uint8_t* st;
     int pp;  // payload row pitch (pb + kRowPad)
     __device__ const uint8_t* row(int t) const { return st + t * pp; }
-    __device__ const uint8_t* meta(int t) const { return st + kTile * pp + t * Traits<F>::MB; }
-    __device__ int id(int t) const {
-        return reinterpret_cast<const int*>(st + kTile * pp + kTile * Traits<F>::MB)[t];
-    }
-    __device__ float scale(int t) const {
-        return reinterpret_cast<const float*>(st + kTile * pp + kTile * Traits<F>::MB + kTile * 4)[t];
-    }
     __device__ uint32_t ids4(int s) const {  // clamped ids of tokens 4s .. 4s+3, one byte each
-        return reinterpret_cast<const uint32_t*>(st + kTile * pp + kTile * Traits<F>::MB + 2 * kTile * 4)[s];
+        return reinterpret_cast<const uint32_t*>(st + kTile * pp)[s];
     }
 };
+
+// The payload dwords of lane (token t, group g) that its decoder reads:
+// INT4 words 2g, 2g+1, 8+2g, 9+2g; INT2 words g, 4+g; 4:16 the 8-byte value
+// words of tiles g and 4+g; structured INT4 words g/2, 2+g/2.  From the
+// staged row.
+template <int F>
+__device__ __forceinline__ void lane_words(const StageView<F>& S, int t, int g, uint32_t* w) {
+    const uint32_t* row = reinterpret_cast<const uint32_t*>(S.row(t));
+    if constexpr (F == D_Q4 || F == D_STRUCT16) {
+        const uint2 a = *reinterpret_cast<const uint2*>(row + 2 * g);
+        const uint2 b = *reinterpret_cast<const uint2*>(row + 8 + 2 * g);
+        w[0] = a.x; w[1] = a.y; w[2] = b.x; w[3] = b.y;
+    } else if constexpr (F == D_Q2) {
+        w[0] = row[g]; w[1] = row[4 + g];
+    } else if constexpr (F == D_SINT4) {
+        w[0] = row[g >> 1]; w[1] = row[2 + (g >> 1)];
+    }
+}
 
 // ---------------------------------------------------------------------------
 // residual decoders.  Lane L = 16 g + t owns token t of the tile and channel
@@ -301,7 +316,6 @@ __host__ __device__ constexpr uint32_t struct_selector(uint32_t v, uint32_t rank
 __device__ __forceinline__ float half_lo(uint32_t w) { return h2f((uint16_t)(w & 0xFFFFu)); }
 __device__ __forceinline__ float half_hi(uint32_t w) { return h2f((uint16_t)(w >> 16)); }
 __device__ __forceinline__ int popc(uint32_t v) { return __builtin_popcount(v); }
-__device__ __forceinline__ int clamp_id(int id, int nc) { return id < 0 ? 0 : (id >= nc ? nc - 1 : id); }
 
 // Kept values of one 4-channel run as two fp16 pairs.  The window's third
 // dword matters only for a full run (pattern 15) starting at an odd rank; it
@@ -333,14 +347,14 @@ constexpr bool kHalfFmt = F == D_BITMAP || F == D_BITMAP_W || F == D_TILED || F 
                           F == D_STRUCT16 || F == D_DENSE;
 
 template <int F>
-__device__ __forceinline__ void residual_h(const StageView<F>& S, int t, int g, int width, GroupMask gm,
-                                           const uint32_t* lut, uint32_t* h) {
+__device__ __forceinline__ void residual_h(const StageView<F>& S, const Prefetch<F>& R, int t, int g, int width,
+                                           GroupMask gm, const uint32_t* lut, uint32_t* h) {
     const uint8_t* row = S.row(t);
     if constexpr (F == D_BITMAP || F == D_BITMAP_W) {
         // words: channels 0..63 in (m.y:m.x), 64..127 in (m.w:m.z), MSB-first
         // (reference.py:22-26); group g's 16 channels are the (g odd ? low : high)
         // half of dword (g < 2 ? high : low), channel 16g + c at field bit 15 - c
-        const uint4 m = lds_ld16(S.meta(t));
+        const uint4 m = R.meta;
         const uint32_t sh = (g & 1) ? 0u : 16u;
         const uint32_t f0 = ((g < 2 ? m.y : m.x) >> sh) & 0xFFFFu;
         const uint32_t f1 = ((g < 2 ? m.w : m.z) >> sh) & 0xFFFFu;
@@ -357,7 +371,7 @@ __device__ __forceinline__ void residual_h(const StageView<F>& S, int t, int g, 
     } else if constexpr (F == D_TILED || F == D_TILED_W || F == D_STRUCT16) {
         // word w = code(tile 2w) | code(tile 2w+1) << 16 (reference.py:36-47);
         // group g covers tiles g and 4 + g
-        const uint4 m = lds_ld16(S.meta(t));
+        const uint4 m = R.meta;
         const uint32_t sh = (uint32_t)(g & 1) * 16u;
         uint32_t f0 = ((g < 2 ? m.x : m.y) >> sh) & 0xFFFFu;
         uint32_t f1 = ((g < 2 ? m.z : m.w) >> sh) & 0xFFFFu;
@@ -371,8 +385,10 @@ __device__ __forceinline__ void residual_h(const StageView<F>& S, int t, int g, 
                 k0 |= 1u << ((f0 >> (4 * j)) & 15u);
                 k1 |= 1u << ((f1 >> (4 * j)) & 15u);
             }
-            const uint2 pa = reinterpret_cast<const uint2*>(row)[g];
-            const uint2 pb = reinterpret_cast<const uint2*>(row)[4 + g];
+            uint32_t w[4];
+            lane_words<F>(S, t, g, w);
+            const uint2 pa = make_uint2(w[0], w[1]);  // tile g's four values
+            const uint2 pb = make_uint2(w[2], w[3]);  // tile 4 + g's
             const uint32_t* slut = lut + kLutWords;
             int r0 = 0, r1 = 0;
 #pragma unroll
@@ -401,7 +417,7 @@ __device__ __forceinline__ void residual_h(const StageView<F>& S, int t, int g, 
             }
         }
     } else if constexpr (F == D_DENSE) {
-        const uint4* r = reinterpret_cast<const uint4*>(row);
+        const uint4* r = reinterpret_cast<const uint4*>(row);  // staged rows
         const uint4 a = lds_ld16(r + 2 * g), b = lds_ld16(r + 2 * g + 1), c = lds_ld16(r + 8 + 2 * g),
                     d = lds_ld16(r + 9 + 2 * g);
         const uint32_t v[16] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w, c.x, c.y, c.z, c.w, d.x, d.y, d.z, d.w};
@@ -410,41 +426,27 @@ __device__ __forceinline__ void residual_h(const StageView<F>& S, int t, int g, 
     }
 }
 
-// Quantised residuals in fp32, value m of the lane's channels.
+// Structured INT4 residuals in fp32, value m of the lane's channels: 1 of 4
+// per subgroup of four channels, 2-bit position, signed nibble code, fp16
+// scale (reference.py:27-35); group g holds subgroups 4g..4g+3 (word g/2 of
+// the payload row) and 16+4g..16+4g+3 (word 2 + g/2).
 template <int F>
-__device__ __forceinline__ void residual_f(const StageView<F>& S, int t, int g, float* r) {
-    const uint8_t* row = S.row(t);
-    const float s = S.scale(t);
-    if constexpr (F == D_Q4 || F == D_Q2) {
-        // signed codes, channel d in word d / (32/bits) at bit (d % (32/bits)) * bits (reference.py:17-21)
-        constexpr int bits = F == D_Q4 ? 4 : 2;
-        constexpr int per_word = 32 / bits;
-        const uint32_t* qw = reinterpret_cast<const uint32_t*>(row);
-        const int wl = (16 * g) / per_word, wh = (64 + 16 * g) / per_word;
+__device__ __forceinline__ void residual_f(const StageView<F>& S, const Prefetch<F>& R, int t, int g, float* r) {
+    static_assert(F == D_SINT4, "structured INT4 only");
+    const float s = h2f(R.sc);
+    const uint2 qm = make_uint2(R.meta.x, R.meta.y);
+    uint32_t w[2];
+    lane_words<F>(S, t, g, w);
 #pragma unroll
-        for (int m = 0; m < 16; ++m) {
-            const int lo = (int)qw[wl + m / per_word], hi = (int)qw[wh + m / per_word];
-            r[m] = (float)(int)__builtin_amdgcn_sbfe(lo, (m % per_word) * bits, bits) * s;
-            r[16 + m] = (float)(int)__builtin_amdgcn_sbfe(hi, (m % per_word) * bits, bits) * s;
-        }
-    } else if constexpr (F == D_SINT4) {
-        // 1 of 4 per subgroup of four channels: 2-bit position, signed nibble
-        // code, fp16 scale (reference.py:27-35); group g holds subgroups
-        // 4g..4g+3 and 16+4g..16+4g+3
-        const uint4 qp = lds_ld16(row);
-        const uint2 qm = *reinterpret_cast<const uint2*>(S.meta(t));
-        const uint32_t qw[4] = {qp.x, qp.y, qp.z, qp.w};
+    for (int u = 0; u < 4; ++u) {
+        const int off = 4 * (4 * (g & 1) + u);
+        const float vl = (float)(int)__builtin_amdgcn_sbfe((int)w[0], off, 4) * s;
+        const float vh = (float)(int)__builtin_amdgcn_sbfe((int)w[1], off, 4) * s;
+        const uint32_t sl = (qm.x >> (2 * (4 * g + u))) & 3u, shh = (qm.y >> (2 * (4 * g + u))) & 3u;
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int off = 4 * (4 * (g & 1) + u);
-            const float vl = (float)(int)__builtin_amdgcn_sbfe((int)qw[g >> 1], off, 4) * s;
-            const float vh = (float)(int)__builtin_amdgcn_sbfe((int)qw[2 + (g >> 1)], off, 4) * s;
-            const uint32_t sl = (qm.x >> (2 * (4 * g + u))) & 3u, shh = (qm.y >> (2 * (4 * g + u))) & 3u;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                r[4 * u + j] = (uint32_t)j == sl ? vl : 0.0f;
-                r[16 + 4 * u + j] = (uint32_t)j == shh ? vh : 0.0f;
-            }
+        for (int j = 0; j < 4; ++j) {
+            r[4 * u + j] = (uint32_t)j == sl ? vl : 0.0f;
+            r[16 + 4 * u + j] = (uint32_t)j == shh ? vh : 0.0f;
         }
     }
 }
@@ -458,17 +460,16 @@ __device__ __forceinline__ void residual_f(const StageView<F>& S, int t, int g, 
 // packed fp16 FMA scales by 2^-k and subtracts 1024 / 2^k + 2^(bits-1),
 // leaving the code.  Every step is exact.
 template <int F>
-__device__ __forceinline__ void code_halves(const StageView<F>& S, int t, int g, uint32_t* h) {
-    const uint32_t* qw = reinterpret_cast<const uint32_t*>(S.row(t));
+__device__ __forceinline__ void code_halves(const StageView<F>& S, const Prefetch<F>& R, int t, int g, uint32_t* h) {
     constexpr uint32_t kMagic = 0x64646464u;
+    uint32_t lw[4];
+    lane_words<F>(S, t, g, lw);
     if constexpr (F == D_Q4) {
         // channel d in word d / 8 at bits 4 (d % 8): pair i of a word is its
         // byte i, low nibble first (reference.py:17-21); words 2g, 2g + 1 hold
         // channels 16g..16g+15 and words 8 + 2g, 9 + 2g channels 64+16g..64+16g+15
         const half2_t mul = {(_Float16)1.0f, (_Float16)0.0625f}, add = {(_Float16)-1032.0f, (_Float16)-72.0f};
-        const uint2 a = *reinterpret_cast<const uint2*>(qw + 2 * g);
-        const uint2 b = *reinterpret_cast<const uint2*>(qw + 8 + 2 * g);
-        const uint32_t w[4] = {a.x, a.y, b.x, b.y};
+        const uint32_t w[4] = {lw[0], lw[1], lw[2], lw[3]};
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             const uint32_t x = w[k] ^ 0x88888888u;
@@ -484,7 +485,7 @@ __device__ __forceinline__ void code_halves(const StageView<F>& S, int t, int g,
         // nibble p; word g holds channels 16g..16g+15, word 4 + g 64+16g..
         const half2_t mul_e = {(_Float16)1.0f, (_Float16)0.25f}, add_e = {(_Float16)-1026.0f, (_Float16)-258.0f};
         const half2_t mul_o = {(_Float16)0.0625f, (_Float16)0.015625f}, add_o = {(_Float16)-66.0f, (_Float16)-18.0f};
-        const uint32_t w[2] = {qw[g], qw[4 + g]};
+        const uint32_t w[2] = {lw[0], lw[1]};
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
             const uint32_t x = w[k] ^ 0xAAAAAAAAu;
@@ -502,11 +503,12 @@ __device__ __forceinline__ void code_halves(const StageView<F>& S, int t, int g,
 // Key values of the lane's 32 channels (pre-RoPE, fp32): centroid + residual.
 // fp16 + fp16 (or fp16 + fp32) sums run as one mixed-precision FMA by `one`.
 template <int F>
-__device__ __forceinline__ void key_values(const StageView<F>& S, int t, int g, int width, GroupMask gm,
-                                           const uint32_t* lut, const uint16_t* s_cent, int nc, float one, float* x) {
+__device__ __forceinline__ void key_values(const StageView<F>& S, const Prefetch<F>& R, int t, int g, int width,
+                                           GroupMask gm, const uint32_t* lut, const uint16_t* s_cent, int nc,
+                                           float one, float* x) {
     uint32_t c[16];
     if constexpr (Traits<F>::CENT) {
-        const int kid = S.id(t);  // clamped when staged
+        const int kid = clamp_id(R.id, nc);  // compression.cu:83-84
         const uint4* cr = reinterpret_cast<const uint4*>(s_cent + kid * kCPitch);
         const uint4 a = lds_ld16(cr + 2 * g), b = lds_ld16(cr + 2 * g + 1), d = lds_ld16(cr + 8 + 2 * g), e = lds_ld16(cr + 9 + 2 * g);
         const uint32_t v[16] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w, d.x, d.y, d.z, d.w, e.x, e.y, e.z, e.w};
@@ -515,7 +517,7 @@ __device__ __forceinline__ void key_values(const StageView<F>& S, int t, int g, 
     }
     if constexpr (kHalfFmt<F>) {
         uint32_t h[16];
-        residual_h<F>(S, t, g, width, gm, lut, h);
+        residual_h<F>(S, R, t, g, width, gm, lut, h);
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             if constexpr (Traits<F>::CENT) {
@@ -529,8 +531,8 @@ __device__ __forceinline__ void key_values(const StageView<F>& S, int t, int g, 
     } else if constexpr (F == D_Q4 || F == D_Q2) {
         // code * scale + centroid: one mixed-precision FMA per channel
         uint32_t h[16];
-        code_halves<F>(S, t, g, h);
-        const float sc = S.scale(t);
+        code_halves<F>(S, R, t, g, h);
+        const float sc = h2f(R.sc);
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             x[2 * i] = __builtin_fmaf(half_lo(h[i]), sc, half_lo(c[i]));
@@ -538,7 +540,7 @@ __device__ __forceinline__ void key_values(const StageView<F>& S, int t, int g, 
         }
     } else {
         float r[32];
-        residual_f<F>(S, t, g, r);
+        residual_f<F>(S, R, t, g, r);
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             x[2 * i] = __builtin_fmaf(half_lo(c[i]), one, r[2 * i]);
@@ -553,20 +555,20 @@ __device__ __forceinline__ void key_values(const StageView<F>& S, int t, int g, 
 // the exact codes for the unstructured formats, fp32 then a conversion for
 // the structured one.
 template <int F>
-__device__ __forceinline__ void value_halves(const StageView<F>& S, int t, int g, int width, GroupMask gm,
-                                             const uint32_t* lut, uint32_t* h) {
+__device__ __forceinline__ void value_halves(const StageView<F>& S, const Prefetch<F>& R, int t, int g, int width,
+                                             GroupMask gm, const uint32_t* lut, uint32_t* h) {
     if constexpr (kHalfFmt<F>) {
-        residual_h<F>(S, t, g, width, gm, lut, h);
+        residual_h<F>(S, R, t, g, width, gm, lut, h);
     } else if constexpr (F == D_Q4 || F == D_Q2) {
         uint32_t c[16];
-        code_halves<F>(S, t, g, c);
-        const _Float16 sh = (_Float16)S.scale(t);  // the stored fp16 scale, exactly
+        code_halves<F>(S, R, t, g, c);
+        const _Float16 sh = __builtin_bit_cast(_Float16, R.sc);  // the stored fp16 scale
         const half2_t s2 = {sh, sh};
 #pragma unroll
         for (int i = 0; i < 16; ++i) h[i] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, c[i]) * s2);
     } else {
         float r[32];
-        residual_f<F>(S, t, g, r);
+        residual_f<F>(S, R, t, g, r);
 #pragma unroll
         for (int i = 0; i < 16; ++i) h[i] = (uint32_t)f2h(r[2 * i]) | ((uint32_t)f2h(r[2 * i + 1]) << 16);
     }
@@ -615,13 +617,38 @@ __device__ __forceinline__ float head_sum(float v) {
 // instruction with a one-hot B operand (the tokens' V clusters against
 // cluster `lane`), which keeps it in registers.
 // ---------------------------------------------------------------------------
+// Waves per SIMD the register allocation aims at: three (at most 168 VGPRs)
+// for the quantised formats, whose decode needs few registers and gains from
+// the third workgroup per CU; two otherwise.
+template <int G, int KF, int VF>
+constexpr int partial_waves() {
+    return (G <= 4 && (KF == D_Q4 || KF == D_Q2) && (VF == D_Q4 || VF == D_Q2)) ? 3 : 1;
+}
+
 template <int G, int KF, int VF, bool TAB>
-__global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(partial_waves<G, KF, VF>())))
+decode_partial_kernel(DParams P) {
     extern __shared__ __align__(16) uint8_t smem[];
     using KT = Traits<KF>;
     using VT = Traits<VF>;
     constexpr int NH = (G + 3) / 4;  // sets of four query heads
-    const int split = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    // One-dimensional grid of splits * H * B workgroups.  Workgroups are
+    // dispatched to the eight XCDs in turn (linear id w on XCD w % 8), each
+    // with its own L2; work items i = (split, head, batch), split-major, are
+    // handed out so that each XCD takes one contiguous block of them, i.e.
+    // whole splits: its workgroups then read the RoPE table rows of their own
+    // share of the positions only, which stays resident in that XCD's L2.
+    int split, h, b;
+    {
+        const int n = (int)gridDim.x, w = (int)blockIdx.x;
+        const int x = w & 7, q = n >> 3, r = n & 7;
+        const int i = x * q + (x < r ? x : r) + (w >> 3);
+        const int pairs = n / P.splits;  // H * B
+        split = i / pairs;
+        const int pr = i - split * pairs;
+        b = pr / P.H;
+        h = pr - b * P.H;
+    }
     const long bh = (long)b * P.H + h;
     const int s0 = (int)(((long)split * P.T) / P.splits);
     const int s1 = (int)(((long)(split + 1) * P.T) / P.splits);
@@ -651,11 +678,10 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
     const WaveSrc<KF> wk = wave_src<KF>(P.k, bh * P.k.ts + t0, t1 - t0);
     const WaveSrc<VF> wv = wave_src<VF>(P.v, bh * P.v.ts + t0, t1 - t0);
     // Tiles are prefetched kDepth ahead into register buffers used in turn
-    // (two for formats of at most one 16-byte piece per lane and tensor, whose
-    // short tiles would otherwise wait on the load latency; one otherwise, and
-    // one for 4:16, whose single buffer brings it to 161 VGPRs and three
-    // workgroups per CU, 4-6% faster at B = 32).
-    constexpr int kDepth = (KT::PQ + VT::PQ <= 2 && G <= 4 && KF != D_STRUCT16) ? 2 : 1;
+    // (two for the quantised formats, whose short tiles would otherwise wait
+    // on the load latency; one for the others, and for G = 8, whose registers
+    // do not allow two).
+    constexpr int kDepth = (KT::DEPTH == 2 && VT::DEPTH == 2 && G <= 4) ? 2 : 1;
     Prefetch<KF> pk[kDepth];
     Prefetch<VF> pv[kDepth];
 #pragma unroll
@@ -745,23 +771,12 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
 
     auto tile_body = [&](int tile, Prefetch<KF>& fk, Prefetch<VF>& fv) {
         const int tb = t0 + tile * kTile;
-        const int n = min(kTile, t1 - tb);
-        stage_store<KF>(fk, st_k, P.k.pb, kslot, lane, P.k.nc);
-        stage_store<VF>(fv, st_v, P.v.pb, vslot, lane, P.v.nc);
-        wave_sync();
-        if (tile + kDepth < ntiles) {
-            prefetch<KF>(wk, P.k.pb, tb + kDepth * kTile - t0, lane, fk);
-            prefetch<VF>(wv, P.v.pb, tb + kDepth * kTile - t0, lane, fv);
-        }
-        // Wave priority rises through the tile (1: key decode, 2: scores and
-        // value decode, 3: softmax and P x V, back to 0 for the next tile's
-        // staging), so that of the two waves sharing a SIMD the one further
-        // through its tile issues first: the pair drifts into complementary
-        // phases, one finishing its matrix-core and softmax tail while the
-        // other decodes (measured: 3% at B = 32 50%, 6-9% at 75%, 3-8% for
-        // the quantised formats).
-        __builtin_amdgcn_s_setprio(1);
-        // position of this lane's key token (padded tokens reuse the last one)
+        const int n = min(kTile, t1 - tb);  // <= 0 for an empty tile
+        // The tile's RoPE table rows are requested first: loads complete in
+        // order, so the wait for them then does not also wait for the next
+        // tiles' prefetch issued below.
+        // position of this lane's key token (padded tokens, and all of an
+        // empty tile's, reuse the wave's last one: start + t1 - 1)
         const int pos = P.start_pos + tb + min(t, n - 1);
         float4 tr[8];
         if constexpr (TAB) {
@@ -773,9 +788,29 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
             for (int i = 0; i < 8; ++i) tr[i] = trow[64 * i];
         }
 
+        stage_store<KF, false>(fk, st_k, P.k.pb, kslot, lane, P.k.nc);
+        stage_store<VF, true>(fv, st_v, P.v.pb, vslot, lane, P.v.nc);
+        wave_sync();
+        // this tile's per-lane registers (metadata, ids, scales)
+        const Prefetch<KF> ck = fk;
+        const Prefetch<VF> cv = fv;
+        // The loads of tile + kDepth go into the buffer just read.  Issued
+        // unconditionally: past the wave's range the buffer loads return zero
+        // without touching memory, and a branch here would make the waits that
+        // follow count the loads as outstanding on one path only.
+        prefetch<KF>(wk, P.k.pb, tb + kDepth * kTile - t0, lane, fk);
+        prefetch<VF>(wv, P.v.pb, tb + kDepth * kTile - t0, lane, fv);
+        // Wave priority rises through the tile (1: key decode, 2: scores and
+        // value decode, 3: softmax and P x V, back to 0 for the next tile's
+        // staging), so that of the two waves sharing a SIMD the one further
+        // through its tile issues first: the pair drifts into complementary
+        // phases, one finishing its matrix-core and softmax tail while the
+        // other decodes (measured: 3% at B = 32 50%, 6-9% at 75%, 3-8% for
+        // the quantised formats).
+        __builtin_amdgcn_s_setprio(1);
         // ---- keys: centroid + residual, rotated ----
         float x[32];
-        key_values<KF>(SK, t, grp, P.k.width, gm, s_lut, s_cent, P.k.nc, P.one, x);
+        key_values<KF>(SK, ck, t, grp, P.k.width, gm, s_lut, s_cent, P.k.nc, P.one, x);
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             float cs4[4], sn4[4];
@@ -819,7 +854,7 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
         // ---- values: residuals as fp16 into the transpose tile ----
         {
             uint32_t hv[16];
-            value_halves<VF>(SV, t, grp, P.v.width, gm, s_lut, hv);
+            value_halves<VF>(SV, cv, t, grp, P.v.width, gm, s_lut, hv);
             uint4* vr = reinterpret_cast<uint4*>(my_vt + t * kVPitch + 16 * grp);
             lds_st16(vr + 0, make_uint4(hv[0], hv[1], hv[2], hv[3]));
             lds_st16(vr + 1, make_uint4(hv[4], hv[5], hv[6], hv[7]));
@@ -905,10 +940,14 @@ __global__ void __launch_bounds__(kThreads) decode_partial_kernel(DParams P) {
         __builtin_amdgcn_s_setprio(0);
         wave_sync();  // stage, tile and weight reads done before the next tile overwrites them
     };
+    // Whole groups of kDepth tiles, with no branch between the tile bodies: a
+    // conditional body makes the load-wait counting conservative at the join,
+    // so that a tile would wait for the loads the previous one issued.  A
+    // tile past the wave's range (at most kDepth - 1 of them, at the end) is
+    // empty: its loads return zero and every one of its tokens is masked.
     for (int tile = 0; tile < ntiles; tile += kDepth) {
 #pragma unroll
-        for (int d = 0; d < kDepth; ++d)
-            if (tile + d < ntiles) tile_body(tile + d, pk[d], pv[d]);
+        for (int d = 0; d < kDepth; ++d) tile_body(tile + d, pk[d], pv[d]);
     }
 
     // ---- per-head totals, then merge the waves through LDS ----
@@ -1589,7 +1628,7 @@ int run_decode(const void* q, int kf, const DTensor& k, int vf, const DTensor& v
     p.pb = p.pd + (long)B * Hq * S * kDim;
     hipStream_t st = (hipStream_t)stream;
     void* args[] = {&p};
-    if (hipLaunchKernel(fn, dim3(S, H, B), dim3(kThreads), args, L.bytes, st) != hipSuccess)
+    if (hipLaunchKernel(fn, dim3((unsigned)((long)S * H * B)), dim3(kThreads), args, L.bytes, st) != hipSuccess)
         return reskv_host::check_launch("decode_partial_kernel");
     if (reskv_host::check_launch("decode_partial_kernel")) return 1;
     if (recent != nullptr) {
