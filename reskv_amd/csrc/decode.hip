@@ -852,7 +852,31 @@ decode_partial_kernel(DParams P) {
         }
 
         // ---- values: residuals as fp16 into the transpose tile ----
-        {
+        if constexpr (VF == D_STRUCT16) {
+            // 4:16: the row's 32 channels are zeroed and each of the lane's
+            // eight kept values is written at the channel its nibble names
+            // (tile g: channels 16g + nibble, tile 4 + g: 64 + 16g + nibble;
+            // the four values of a tile are one 8-byte word, reference.py:36-47)
+            uint16_t* vr = my_vt + t * kVPitch + 16 * grp;
+            const uint4 z = make_uint4(0u, 0u, 0u, 0u);
+            lds_st16(vr, z);
+            lds_st16(vr + 8, z);
+            lds_st16(vr + 64, z);
+            lds_st16(vr + 72, z);
+            const uint32_t sh = (uint32_t)(grp & 1) * 16u;
+            const uint32_t c0 = ((grp < 2 ? cv.meta.x : cv.meta.y) >> sh) & 0xFFFFu;
+            const uint32_t c1 = ((grp < 2 ? cv.meta.z : cv.meta.w) >> sh) & 0xFFFFu;
+            const uint32_t* row = reinterpret_cast<const uint32_t*>(SV.row(t));
+            const uint2 pa = *reinterpret_cast<const uint2*>(row + 2 * grp);
+            const uint2 pb = *reinterpret_cast<const uint2*>(row + 8 + 2 * grp);
+            const uint32_t va[4] = {pa.x, pa.x >> 16, pa.y, pa.y >> 16};
+            const uint32_t vb[4] = {pb.x, pb.x >> 16, pb.y, pb.y >> 16};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                vr[(c0 >> (4 * j)) & 15u] = (uint16_t)va[j];
+                vr[64 + ((c1 >> (4 * j)) & 15u)] = (uint16_t)vb[j];
+            }
+        } else {
             uint32_t hv[16];
             value_halves<VF>(SV, cv, t, grp, P.v.width, gm, s_lut, hv);
             uint4* vr = reinterpret_cast<uint4*>(my_vt + t * kVPitch + 16 * grp);
