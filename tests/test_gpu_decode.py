@@ -119,14 +119,18 @@ def test_residual_widths_through_family_ops(device, fmt, width):
         assert _max_err(out.view(b, hk * g, 1, 128), ref) <= ATOL, splits
 
 
-@pytest.mark.parametrize("bits,sparsity,layout,b,t,inputs", [(16, 0.5, "unstructured", 32, 8192, "sweep"),
-                                                             (16, 0.75, "structured", 32, 8192, "sweep"),
-                                                             (4, 0.5, "unstructured", 8, 16384, "outlier"),
-                                                             (2, 0.5, "unstructured", 8, 16384, "outlier")])
+@pytest.mark.parametrize("bits,sparsity,layout,b,t,inputs",
+                         [(16, 0.5, "unstructured", bb, 8192, "sweep") for bb in (1, 4, 8, 16, 32)]
+                         + [(16, 0.75, "structured", bb, 8192, "sweep") for bb in (1, 4, 8, 16, 32)]
+                         + [(4, 0.5, "unstructured", 8, 16384, "outlier"),
+                            (2, 0.5, "unstructured", 8, 16384, "outlier")])
 def test_benchmark_shapes_against_fp32_checker(device, bits, sparsity, layout, b, t, inputs):
     """Configs 2 and 3 at their full shapes (Hq = 32, Hk = 8): the split-K decode at the
     automatic split count and at 16 splits against the float32 torch port of the oracle
-    (oracle/torch_checker.py, pinned to the oracle's golden vectors on the CPU).
+    (oracle/torch_checker.py, pinned to the oracle's golden vectors on the CPU).  Config 2
+    runs at every batch of its sweep (1, 4, 8, 16, 32), so each automatic split count and
+    kernel instance the bench times (64 / 16 / 8 / 4 / 2 splits at 50%; the 4:16 instance
+    at two and three workgroups per CU) is checked at T = 8192.
 
     Config 2 uses the timing sweep's inputs (0.5 N(0,1) K and V, 0.1 N(0,1) centres,
     random ids; reskv benchmarks/kernels.py:57-65).  Config 3 uses its own recipe:
