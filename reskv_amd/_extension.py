@@ -82,8 +82,8 @@ def _workspace(nbytes, device):
 #
 # A caller's inv_freq tensor is matched to its content key through
 # _BY_TENSOR (storage address, offset and dtype; the version counter detects
-# in-place updates), whose entry is dropped by a finalizer when that tensor is
-# collected, so a reused address never maps to
+# in-place updates, except for inference tensors, which have none), whose
+# entry is dropped by a finalizer when that tensor is collected, so a reused address never maps to
 # a stale key; a tensor not seen before costs one 256-byte device-to-host copy
 # of its values.  Fresh tensors with equal values (a per-call `.float()` of an
 # fp16 buffer, a `.to(device)` copy) therefore share one table.
@@ -130,12 +130,15 @@ def _table_for(key, freq, positions):
 
 def _content_key(inv_freq, dev):
     ident = (dev, inv_freq.untyped_storage().data_ptr(), inv_freq.storage_offset(), inv_freq.dtype)
+    # inference tensors carry no version counter: an in-place update of one is
+    # not seen (pass a new tensor instead)
+    version = -1 if inv_freq.is_inference() else inv_freq._version
     seen = _BY_TENSOR.get(ident)
-    if seen is not None and seen[0] == inv_freq._version:
+    if seen is not None and seen[0] == version:
         return seen[1]
     values = inv_freq.detach().reshape(64).to(device="cpu", dtype=torch.float32)
     key = (dev, "freq", values.numpy().tobytes())
-    _BY_TENSOR[ident] = (inv_freq._version, key)  # an in-place update replaces the entry
+    _BY_TENSOR[ident] = (version, key)  # an in-place update replaces the entry
     if seen is None:
         weakref.finalize(inv_freq, _BY_TENSOR.pop, ident, None)
     return key

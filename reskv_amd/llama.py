@@ -184,9 +184,10 @@ class RandomLlama:
             self.layers.append({
                 "wqkv": w(s.hidden + 2 * kvd, s.hidden), "wo": w(s.hidden, s.hidden),
                 "wgu": w(2 * s.ffn, s.hidden), "wd": w(s.hidden, s.ffn),
-                "n1": torch.ones(s.hidden, device=dev), "n2": torch.ones(s.hidden, device=dev),
+                "n1": torch.ones(s.hidden, device=dev, dtype=torch.float16),
+                "n2": torch.ones(s.hidden, device=dev, dtype=torch.float16),
             })
-        self.norm = torch.ones(s.hidden, device=dev)
+        self.norm = torch.ones(s.hidden, device=dev, dtype=torch.float16)
         self.lm_head = w(s.vocab, s.hidden)
         self.inv_freq = llama3_inv_freq(s).to(dev)
         self.scaling = s.head_dim ** -0.5
@@ -215,10 +216,11 @@ class RandomLlama:
             flat[r0: r0 + rows] += F.linear(act, p["wd"])
 
     @torch.no_grad()
-    def prefill(self, ids, sink, q_rows=2048):
+    def prefill(self, ids, sink, q_rows=2048, logits=False):
         """Causal forward of the prompt ids [B, T]; ``sink(layer, raw_k, rot_k, v)``
         receives each layer's keys and values as [B, Hk, T, 128].  Returns the
-        greedy next token per sequence [B]."""
+        greedy next token per sequence [B] (or, with ``logits``, the last
+        position's logits [B, vocab])."""
         s = self.shape
         b, t = ids.shape
         cos, sin = self.rope_tables(t)
@@ -251,7 +253,8 @@ class RandomLlama:
             del attn
             self._mlp(x, p)
         last = _rmsnorm(x[:, -1], self.norm, s.rms_eps)
-        return torch.argmax(F.linear(last, self.lm_head), dim=-1)
+        out = F.linear(last, self.lm_head)
+        return out if logits else torch.argmax(out, dim=-1)
 
 
 class GreedyDecoder:

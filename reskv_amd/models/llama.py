@@ -119,9 +119,27 @@ class ResKVForCausalLM(LlamaForCausalLM):
             kwargs["kernel_config"] = kernel_config
         return super().from_pretrained(pretrained_model_name_or_path, *args, **kwargs)
 
+    def _apply(self, fn, recurse=True):
+        """Module moves and casts (``.half()``, ``.to()``, ``.cuda()``) keep the
+        rotary inverse frequencies in fp32: rounded to fp16 they would move every
+        RoPE angle of the prompt pass, away from the fp32 angles of the
+        compressed decode, and a reload (which keeps them fp32) would compute
+        different logits."""
+        rotary = getattr(getattr(self, "model", None), "rotary_emb", None)
+        keep = {}
+        if rotary is not None:
+            keep = {n: b for n, b in rotary._buffers.items()
+                    if b is not None and "inv_freq" in n and b.dtype == torch.float32}
+        out = super()._apply(fn, recurse)
+        for n, b in keep.items():
+            cur = rotary._buffers[n]
+            if cur is not None and cur.dtype != torch.float32:
+                rotary._buffers[n] = b.to(cur.device)
+        return out
+
     def _model_frequencies(self):
-        """The rotary inverse frequencies in fp32; recomputed once when ``.half()``
-        has rounded the buffer (rounded values would move every angle)."""
+        """The rotary inverse frequencies in fp32 (recomputed once if the buffer
+        arrived rounded, e.g. from a checkpoint stored that way)."""
         rotary = self.model.rotary_emb
         if rotary.inv_freq.dtype == torch.float32:
             return rotary.inv_freq

@@ -111,3 +111,21 @@ def test_dense_first_step_attention_matches_fp32(device):
     w = torch.softmax(torch.einsum("bhd,bhtd->bht", q, kr) * model.scaling, -1)
     ref = torch.einsum("bht,bhtd->bhd", w, v)
     assert (dec.attn.float() - ref).abs().max().item() <= 2e-3
+
+
+@pytest.mark.gpu
+def test_fused_decode_step_equals_the_torch_forward(device):
+    """One graph-replayed decode step of the harness (fused RMSNorm, QKV split and
+    rotation, gated activation, residual adds in the GEMMs, dense attention) gives
+    the logits of the plain torch forward over the prompt plus that token."""
+    model = RandomLlama(TINY, "cuda", seed=5)
+    ids = torch.randint(128, TINY.vocab, (2, 96), generator=torch.Generator().manual_seed(6)).cuda()
+    dec = GreedyDecoder(model, 2, 96, 4, "dense")
+    first = model.prefill(ids, dec.absorb, q_rows=64)
+    dec.start(first)
+    dec.step()
+    got = torch.nn.functional.linear(dec.h, model.lm_head).float()  # the head graph's normed hidden
+    ref = model.prefill(torch.cat((ids, first[:, None]), 1), lambda *a: None, q_rows=64, logits=True).float()
+    scale = ref.abs().max().item()
+    assert (got - ref).abs().max().item() <= 2e-2 * scale
+    assert torch.equal(dec.tok, ref.argmax(-1))

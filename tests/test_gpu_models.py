@@ -67,3 +67,56 @@ def test_generate_over_compressed_history(device, monkeypatch, sparsity, rope):
         assert freq is not None and freq.dtype == torch.float32
         ref = expected_attention(q, comp, position=position, inv_freq=freq, scaling=scaling, recent=ring)
         assert float(abs(np_(got).astype("float64") - ref).max()) <= ATOL
+
+
+def _small_llama():
+    return LlamaConfig(hidden_size=512, intermediate_size=1024, num_hidden_layers=2, num_attention_heads=4,
+                       num_key_value_heads=1, vocab_size=256, max_position_embeddings=8192, rope_theta=500000.0)
+
+
+@pytest.mark.parametrize("bits,sparsity", [(16, 0.5), (16, 0.75), (4, 0.5), (4, 0.75), (2, 0.5)])
+def test_plans_through_generate_and_save_reload(device, tmp_path, monkeypatch, bits, sparsity):
+    """Every residual format through transformers' generate across group
+    compressions, then save/reload with equal logits (reskv tests/test_model.py:29-58:
+    96-token prompt, recent window 16, groups of 32, 4 clusters of at most 8, 66 new
+    tokens, i.e. two group compressions after the prefill split).  The attention the
+    model computes over the compressed history is checked against the float64
+    oracle at the first decode steps and after each group compression."""
+    torch.manual_seed(9)
+    settings = ResKVKernelConfig(bits=bits, sparsity=sparsity, layout="auto", recent_size=16, group_size=32,
+                                 num_clusters=4, max_clusters=8)
+    model = ResKVForCausalLM(_small_llama(), settings).cuda().half().eval()
+    checked = []  # (compressed length, position, max-abs error against the oracle)
+    first_layer = []
+    original = ResKVLayerCache.attend
+
+    def recording(self, query, query_rot, *, scaling, inv_freq=None, rope_theta=500000.0):
+        out = original(self, query, query_rot, scaling=scaling, inv_freq=inv_freq, rope_theta=rope_theta)
+        if not first_layer:
+            first_layer.append(self)  # the first attend of a decode step is layer 0's
+        comp = self.compressed
+        if self is first_layer[0] and (len(checked) < 2 or checked[-1][0] != comp.seq_len):
+            assert comp.key.plan == settings.resolve(1)
+            ring = (query_rot, self.keys[:, :, : self.live], self.values[:, :, : self.live])
+            ref = expected_attention(query, comp, position=self.length - 1, inv_freq=inv_freq, scaling=scaling,
+                                     recent=ring)
+            checked.append((comp.seq_len, self.length - 1, float(abs(np_(out).astype("float64") - ref).max())))
+        return out
+
+    monkeypatch.setattr(ResKVLayerCache, "attend", recording)
+    x = torch.randint(10, 200, (1, 96), device=device)
+    with torch.inference_mode():
+        initial = model(x, use_cache=True)
+        cache = initial.past_key_values
+        assert cache.layers[0].compressed.key.plan == settings.resolve(1)
+        result = model.generate(x, max_new_tokens=66, do_sample=False, eos_token_id=None, pad_token_id=0)
+    assert result.shape == (1, 162)
+    assert len({c[0] for c in checked}) >= 3  # the prefill split and two group compressions
+    for length, position, err in checked:
+        assert err <= ATOL, (length, position, err)
+    model.save_pretrained(tmp_path)
+    restored = ResKVForCausalLM.from_pretrained(tmp_path, dtype=torch.float16).cuda().eval()
+    assert restored.kernel_config == settings
+    assert restored.config.reskv_kernel_config == settings.to_dict()
+    with torch.inference_mode():
+        torch.testing.assert_close(initial.logits, restored(x, use_cache=True).logits)

@@ -94,3 +94,19 @@ def test_from_pretrained_takes_the_kernel_config(tmp_path):
     model.save_pretrained(tmp_path / "saved")
     reloaded = ResKVForCausalLM.from_pretrained(tmp_path / "saved")  # settings stored with the checkpoint
     assert reloaded.kernel_config == cfg
+
+
+def test_half_keeps_the_rotary_frequencies_in_fp32(tmp_path):
+    """``.half()`` casts every buffer; the rotary inverse frequencies stay fp32
+    (equal to those of a reload with dtype=float16), so the prompt pass and the
+    compressed decode rotate with the same angles and reloaded logits agree."""
+    import torch
+
+    model = ResKVForCausalLM(_config()).half().eval()
+    rotary = model.model.rotary_emb
+    assert rotary.inv_freq.dtype == torch.float32
+    assert model.model.layers[0].mlp.gate_proj.weight.dtype == torch.float16
+    model.save_pretrained(tmp_path)
+    again = ResKVForCausalLM.from_pretrained(tmp_path, dtype=torch.float16)
+    assert torch.equal(again.model.rotary_emb.inv_freq, rotary.inv_freq)
+    assert torch.equal(model._model_frequencies(), rotary.inv_freq)

@@ -94,3 +94,14 @@ def test_theta_sets_are_keyed_by_theta(builds):
 def test_rejects_a_wrong_frequency_count(builds):
     with pytest.raises(RuntimeError, match="inv_freq"):
         ext._rope(torch.ones(32), 10000.0, "cpu", 1024)
+
+
+def test_inference_tensors_are_keyed_without_a_version(builds):
+    """Tensors made under torch.inference_mode have no version counter (the
+    model patch runs generate under it); they are keyed by address alone."""
+    with torch.inference_mode():
+        f = _freq()
+        freq, t1 = ext._rope(f, 10000.0, "cpu", 1024)
+        _, t2 = ext._rope(f, 10000.0, "cpu", 1024)
+        _, t3 = ext._rope(_freq(), 10000.0, "cpu", 1024)  # fresh tensor, equal values
+    assert t1 is t2 is t3 and len(builds) == 1 and torch.equal(freq, _freq())
