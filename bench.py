@@ -27,6 +27,7 @@ import sys
 import time
 
 HBM_PEAK = 8.0e12  # bytes/s, MI355X HBM3E
+FP16_MFMA_PEAK_TFLOPS = 2500.0  # dense fp16 matrix-core peak of an MI355X
 METRIC = "decode tok/s, Llama-3.1-8B-shape 8K ctx bs1-32; attn µs/step + % HBM peak"
 LAYERS = 32
 HQ, HK, D, T = 32, 8, 128, 8192
@@ -262,8 +263,20 @@ def measure_encoders(torch, device, reps=20):
     us_v = timed(lambda: cluster(v, 32, 10, value=True), max(3, reps // 4), 2)
     us_kv = timed(lambda: cluster_kv(k, v, 32, 10), max(3, reps // 4), 2)
     flop = 2.0 * t * 32 * D * h * 10
+    # matrix-core work the kernels issue per iteration and head: K takes the
+    # distance product twice (fp16 hi and lo parts of its fp32 centres), V once;
+    # both add the one-hot member sums (2 T C D) and counts (2 T C 16)
+    mfma_k = (6.0 * t * 32 * D + 2.0 * t * 32 * 16) * h * 10
+    mfma_v = (4.0 * t * 32 * D + 2.0 * t * 32 * 16) * h * 10
     out["kmeans"] = {"us_k": us_k, "us_v": us_v, "us_kv_together": us_kv, "tflops_k": flop / us_k / 1e6,
-                     "tflops_v": flop / us_v / 1e6, "iterations": 10, "clusters": 32}
+                     "tflops_v": flop / us_v / 1e6, "iterations": 10, "clusters": 32,
+                     "mfma_tflops_kv": (mfma_k + mfma_v) / us_kv / 1e6,
+                     "mfma_util": (mfma_k + mfma_v) / us_kv / 1e6 / FP16_MFMA_PEAK_TFLOPS,
+                     "algorithmic_frac_of_fp16_peak": 2 * flop / us_kv / 1e6 / FP16_MFMA_PEAK_TFLOPS,
+                     "mfma_note": "mfma_util: fp16 matrix-core FLOP issued (K: hi and lo distance products, "
+                                  "V: one; one-hot member sums and counts) per second of the paired K+V run, "
+                                  "over the 2.5 PFLOP/s dense fp16 peak; algorithmic: the distance FLOP "
+                                  "2 T C D alone"}
     n_in = b * h * t * (D * 2 + 4) + b * h * 32 * D * 2
     # K and V encoded in one launch, as compress runs them
     cases = (("structured_fp16_75", 32 * 2 + 16, lambda: ext.compress_fp16_kv(k, kc, ki, v, vc, vi, 32, True)),
@@ -344,15 +357,30 @@ def measure_e2e(torch, device, batch=16, prompt=8192, steps=2048, warmup=4, attn
     decs = {"reskv": GreedyDecoder(model, batch, prompt, total, "reskv", cfg),
             "dense_fp16": GreedyDecoder(model, batch, prompt, total, "dense")}
 
+    compress_events = []
+
     def sink(layer, raw_k, rot_k, v):
-        for d in decs.values():
-            d.absorb(layer, raw_k, rot_k, v)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        decs["reskv"].absorb(layer, raw_k, rot_k, v)  # K-means, encoders, ring copy of this layer
+        e1.record()
+        compress_events.append((e0, e1))
+        decs["dense_fp16"].absorb(layer, raw_k, rot_k, v)
 
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     first = model.prefill(ids, sink)
     torch.cuda.synchronize()
-    out = {"prefill_s_incl_compression": time.perf_counter() - t0, "batch": batch, "prompt": prompt,
+    prefill_s = time.perf_counter() - t0
+    compress_ms = [a.elapsed_time(b) for a, b in compress_events]
+    out = {"prefill_s_incl_compression": prefill_s,
+           "prefill_compression_ms_per_layer": sum(compress_ms) / len(compress_ms),
+           "prefill_compression_s_total": sum(compress_ms) / 1e3,
+           "prefill_s_without_compression": prefill_s - sum(compress_ms) / 1e3,
+           "prefill_compression_note": "GPU time between events around each layer's ResKV cache hand-off "
+                                       "(K-means of K and V, residual encoders, ring copy) during the prompt "
+                                       "forward; the dense cache's copy is outside it",
+           "batch": batch, "prompt": prompt,
            "new_tokens_timed": steps, "config4_new_tokens": 2048,
            "note": (f"decode rates timed over {steps} greedy tokens after {warmup} warm-up tokens"
                     + ("" if steps == 2048 else f" (config 4 names 2048; the per-token work is the same, "
