@@ -272,7 +272,7 @@ __device__ __forceinline__ void lane_words(const StageView<F>& S, int t, int g, 
 //
 // A group's channels are four runs of four.  The kept values of a run are
 // consecutive in the payload row, starting at rank `base`; the 8-byte window at
-// `base` is fetched with two dword reads plus an alignbit, and one v_perm per
+// `base` is fetched with dword reads plus an alignbit, and one v_perm per
 // channel pair scatters the window's halves onto the kept channels (zeros
 // elsewhere).  The permute selectors depend only on the run's 4-bit keep
 // pattern and come from a 16-entry table in LDS (one table for MSB-first
@@ -317,20 +317,35 @@ __device__ __forceinline__ float half_lo(uint32_t w) { return h2f((uint16_t)(w &
 __device__ __forceinline__ float half_hi(uint32_t w) { return h2f((uint16_t)(w >> 16)); }
 __device__ __forceinline__ int popc(uint32_t v) { return __builtin_popcount(v); }
 
-// Kept values of one 4-channel run as two fp16 pairs.  The window's third
-// dword matters only for a full run (pattern 15) starting at an odd rank; it
-// is read unconditionally (a read past a row's pad stays inside the stage: the
-// next row, or the metadata after the last row), so the runs stay branch-free
-// and their LDS reads can be issued together.
-__device__ __forceinline__ void run_h(const uint8_t* row, int base, const uint32_t* tab, uint32_t v, uint32_t* out) {
-    const uint32_t* dw = reinterpret_cast<const uint32_t*>(row) + (base >> 1);
-    const uint32_t d0 = dw[0], d1 = dw[1], d2 = dw[2];
-    const uint32_t sh = (uint32_t)(base & 1) * 16u;
-    const uint32_t w0 = __builtin_amdgcn_alignbit(d1, d0, sh);
-    const uint32_t w1 = __builtin_amdgcn_alignbit(d2, d1, sh);
-    const uint2 sel = *reinterpret_cast<const uint2*>(tab + 2 * v);
-    out[0] = __builtin_amdgcn_perm(w1, w0, sel.x);
-    out[1] = __builtin_amdgcn_perm(w1, w0, sel.y);
+// Four consecutive runs of a lane's half-group, patterns pat[0..3], the first
+// at rank r.  A run's third window dword matters only for a full run at an
+// odd rank; the next run then starts four ranks on, so that dword is the next
+// run's first one.  Each run therefore reads two dwords and the group one more
+// for its last run (36 bytes instead of 48).
+__device__ __forceinline__ void runs4_h(const uint8_t* row, int r, const uint32_t* tab, const uint32_t* pat,
+                                        uint32_t* out) {
+    const uint32_t* base = reinterpret_cast<const uint32_t*>(row);
+    int rk[4];
+    rk[0] = r;
+#pragma unroll
+    for (int u = 0; u < 3; ++u) rk[u + 1] = rk[u] + popc(pat[u]);
+    uint32_t d0[4], d1[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        d0[u] = base[rk[u] >> 1];
+        d1[u] = base[(rk[u] >> 1) + 1];
+    }
+    const uint32_t dlast = base[(rk[3] >> 1) + 2];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const uint32_t d2 = u < 3 ? d0[u + 1] : dlast;
+        const uint32_t sh = (uint32_t)(rk[u] & 1) * 16u;
+        const uint32_t w0 = __builtin_amdgcn_alignbit(d1[u], d0[u], sh);
+        const uint32_t w1 = __builtin_amdgcn_alignbit(d2, d1[u], sh);
+        const uint2 sel = *reinterpret_cast<const uint2*>(tab + 2 * pat[u]);
+        out[2 * u] = __builtin_amdgcn_perm(w1, w0, sel.x);
+        out[2 * u + 1] = __builtin_amdgcn_perm(w1, w0, sel.y);
+    }
 }
 
 // Bits of a bitmap word's channels that come before group g (channel d sits at
@@ -358,16 +373,16 @@ __device__ __forceinline__ void residual_h(const StageView<F>& S, const Prefetch
         const uint32_t sh = (g & 1) ? 0u : 16u;
         const uint32_t f0 = ((g < 2 ? m.y : m.x) >> sh) & 0xFFFFu;
         const uint32_t f1 = ((g < 2 ? m.w : m.z) >> sh) & 0xFFFFu;
-        int r0 = popc(m.y & gm.hi) + popc(m.x & gm.lo);
-        int r1 = popc(m.y) + popc(m.x) + popc(m.w & gm.hi) + popc(m.z & gm.lo);
+        const int r0 = popc(m.y & gm.hi) + popc(m.x & gm.lo);
+        const int r1 = popc(m.y) + popc(m.x) + popc(m.w & gm.hi) + popc(m.z & gm.lo);
+        uint32_t pa[4], pc[4];
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-            const uint32_t a = (f0 >> (12 - 4 * u)) & 15u, c = (f1 >> (12 - 4 * u)) & 15u;
-            run_h(row, r0, lut, a, h + 2 * u);
-            run_h(row, r1, lut, c, h + 8 + 2 * u);
-            r0 += popc(a);
-            r1 += popc(c);
+            pa[u] = (f0 >> (12 - 4 * u)) & 15u;
+            pc[u] = (f1 >> (12 - 4 * u)) & 15u;
         }
+        runs4_h(row, r0, lut, pa, h);
+        runs4_h(row, r1, lut, pc, h + 8);
     } else if constexpr (F == D_TILED || F == D_TILED_W || F == D_STRUCT16) {
         // word w = code(tile 2w) | code(tile 2w+1) << 16 (reference.py:36-47);
         // group g covers tiles g and 4 + g
@@ -406,15 +421,14 @@ __device__ __forceinline__ void residual_h(const StageView<F>& S, const Prefetch
             }
         } else {
             const int per_tile = width >> 3;
-            int r0 = g * per_tile, r1 = (4 + g) * per_tile;
+            uint32_t pa[4], pc[4];
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
-                const uint32_t a = (f0 >> (4 * u)) & 15u, c = (f1 >> (4 * u)) & 15u;
-                run_h(row, r0, lut + 32, a, h + 2 * u);
-                run_h(row, r1, lut + 32, c, h + 8 + 2 * u);
-                r0 += popc(a);
-                r1 += popc(c);
+                pa[u] = (f0 >> (4 * u)) & 15u;
+                pc[u] = (f1 >> (4 * u)) & 15u;
             }
+            runs4_h(row, g * per_tile, lut + 32, pa, h);
+            runs4_h(row, (4 + g) * per_tile, lut + 32, pc, h + 8);
         }
     } else if constexpr (F == D_DENSE) {
         const uint4* r = reinterpret_cast<const uint4*>(row);  // staged rows
@@ -553,7 +567,9 @@ __device__ __forceinline__ void key_values(const StageView<F>& S, const Prefetch
 // FP16 formats hand their payload halves through unchanged.  Quantised codes
 // times the fp16 scale are rounded once to fp16: one packed fp16 multiply of
 // the exact codes for the unstructured formats, fp32 then a conversion for
-// the structured one.
+// the structured one.  (Folding the Value scale into the softmax weight
+// instead, fp16(p * scale) times the exact codes, measured no faster: the
+// second weight tile's LDS traffic takes what the multiplies save.)
 template <int F>
 __device__ __forceinline__ void value_halves(const StageView<F>& S, const Prefetch<F>& R, int t, int g, int width,
                                              GroupMask gm, const uint32_t* lut, uint32_t* h) {
@@ -663,6 +679,7 @@ decode_partial_kernel(DParams P) {
 
     uint16_t* s_cent = reinterpret_cast<uint16_t*>(smem);  // region 0: fp16 key centroids [nc][kCPitch]
     uint32_t* s_lut = reinterpret_cast<uint32_t*>(smem + P.lut_off);
+    // per wave: fp16 weights [4-token group][head][token] and the V tile [token][kVPitch]
     // per wave: fp16 weights [4-token group][head][token] and the V tile [token][kVPitch]
     uint16_t* my_p = reinterpret_cast<uint16_t*>(smem + P.p_off) + wave * (kTile * G + kTile * kVPitch);
     uint16_t* my_vt = my_p + kTile * G;
