@@ -281,6 +281,7 @@ __device__ __forceinline__ void lane_words(const StageView<F>& S, int t, int g, 
 // ---------------------------------------------------------------------------
 constexpr int kLutWords = 64;        // [msb|lsb][pattern][lo|hi]
 constexpr int kStructLutWords = 160;  // 4:16 tiles: [start rank 0..4][pattern][lo|hi]
+constexpr int kQTrigWords = 128;      // cos, then sin, of the query position for the 64 RoPE pairs
 
 // v_perm selector bytes placing window halves on channels 0..3 of a run
 // (byte 12 selects zero).  msb: pattern bit 3-j = channel j (bitmaps);
@@ -711,6 +712,17 @@ decode_partial_kernel(DParams P) {
         }
     }
 
+    // cos and sin of the query position, once per workgroup (one pair per
+    // thread of the first wave); every lane reads its group's 16 after the
+    // barrier below.  The region follows the permute tables and is not
+    // written again.
+    float* s_qtrig = reinterpret_cast<float*>(s_lut + kLutWords + kStructLutWords);
+    if (threadIdx.x < kHalf) {
+        float sn, cs;
+        rope_sincos_fast(__fmul_rn((float)P.pos_q, P.inv_freq[threadIdx.x]), sn, cs);
+        s_qtrig[threadIdx.x] = cs;
+        s_qtrig[kHalf + threadIdx.x] = sn;
+    }
     if (threadIdx.x < kLutWords) {
         const uint32_t i = threadIdx.x;
         s_lut[i] = perm_selector((i >> 1) & 15u, i < 32, (int)(i & 1));
@@ -725,7 +737,7 @@ decode_partial_kernel(DParams P) {
             lds_st16(s_cent + (i >> 4) * kCPitch + 8 * (i & 15), kc[i]);
     }
 
-    // rotated, pre-scaled query values of this lane's channels for heads 4 hs + hj
+    // frequencies of this lane's 16 pairs (the keys' angles without a table)
     float fr[16];
     {
         const float4* fq = reinterpret_cast<const float4*>(P.inv_freq + 16 * grp);
@@ -738,32 +750,23 @@ decode_partial_kernel(DParams P) {
             fr[4 * u + 3] = f.w;
         }
     }
-    float qv[NH][32];
-    {
-        float sn[16], cs[16];
+    // the query rows of this lane's channels (fp16 pairs), loaded before the
+    // barrier; rotated and pre-scaled for heads 4 hs + hj after it
+    uint32_t qlo[NH][8], qhi[NH][8];
 #pragma unroll
-        for (int m = 0; m < 16; ++m) rope_sincos_fast(__fmul_rn((float)P.pos_q, fr[m]), sn[m], cs[m]);
+    for (int hs = 0; hs < NH; ++hs) {
+        const int g = 4 * hs + hj;
 #pragma unroll
-        for (int hs = 0; hs < NH; ++hs) {
-            const int g = 4 * hs + hj;
-            uint32_t lo[8] = {0, 0, 0, 0, 0, 0, 0, 0}, hi[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-            if (g < G) {
-                const uint4* qr = reinterpret_cast<const uint4*>(P.q + ((long)b * P.Hq + (long)h * G + g) * kDim);
-                const uint4 a = qr[2 * grp], c = qr[2 * grp + 1], d = qr[8 + 2 * grp], e = qr[9 + 2 * grp];
-                const uint32_t vl[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
-                const uint32_t vh[8] = {d.x, d.y, d.z, d.w, e.x, e.y, e.z, e.w};
+        for (int i = 0; i < 8; ++i) qlo[hs][i] = qhi[hs][i] = 0u;
+        if (g < G) {
+            const uint4* qr = reinterpret_cast<const uint4*>(P.q + ((long)b * P.Hq + (long)h * G + g) * kDim);
+            const uint4 a = qr[2 * grp], c = qr[2 * grp + 1], d = qr[8 + 2 * grp], e = qr[9 + 2 * grp];
+            const uint32_t vl[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
+            const uint32_t vh[8] = {d.x, d.y, d.z, d.w, e.x, e.y, e.z, e.w};
 #pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    lo[i] = vl[i];
-                    hi[i] = vh[i];
-                }
-            }
-#pragma unroll
-            for (int m = 0; m < 16; ++m) {
-                const float a = (m & 1) ? half_hi(lo[m >> 1]) : half_lo(lo[m >> 1]);
-                const float c = (m & 1) ? half_hi(hi[m >> 1]) : half_lo(hi[m >> 1]);
-                qv[hs][m] = (a * cs[m] - c * sn[m]) * P.qscale;
-                qv[hs][16 + m] = (c * cs[m] + a * sn[m]) * P.qscale;
+            for (int i = 0; i < 8; ++i) {
+                qlo[hs][i] = vl[i];
+                qhi[hs][i] = vh[i];
             }
         }
     }
@@ -785,6 +788,26 @@ decode_partial_kernel(DParams P) {
     stage_slots<KF>(P.k.pb, lane, kslot);
     stage_slots<VF>(P.v.pb, lane, vslot);
     __syncthreads();
+
+    float qv[NH][32];
+    {
+        float sn[16], cs[16];
+#pragma unroll
+        for (int m = 0; m < 16; ++m) {
+            cs[m] = s_qtrig[16 * grp + m];
+            sn[m] = s_qtrig[kHalf + 16 * grp + m];
+        }
+#pragma unroll
+        for (int hs = 0; hs < NH; ++hs) {
+#pragma unroll
+            for (int m = 0; m < 16; ++m) {
+                const float a = (m & 1) ? half_hi(qlo[hs][m >> 1]) : half_lo(qlo[hs][m >> 1]);
+                const float c = (m & 1) ? half_hi(qhi[hs][m >> 1]) : half_lo(qhi[hs][m >> 1]);
+                qv[hs][m] = (a * cs[m] - c * sn[m]) * P.qscale;
+                qv[hs][16 + m] = (c * cs[m] + a * sn[m]) * P.qscale;
+            }
+        }
+    }
 
     auto tile_body = [&](int tile, Prefetch<KF>& fk, Prefetch<VF>& fv) {
         const int tb = t0 + tile * kTile;
@@ -1364,17 +1387,31 @@ __global__ void __launch_bounds__(kMergeThreads) decode_merge_kernel(
         s_beta[c] = beta;
     }
     __syncthreads();
-    // 5) fold sum_c beta_c c_v[c], normalise (threads 0..127: one channel each)
+    // 5) fold sum_c beta_c c_v[c] by all threads: channel pair tid % 64 over
+    // the centroids c = tid / 64 (mod 4), the four quarters then summed per
+    // channel through the (now unused) cluster-mass table
+    float* s_f = reinterpret_cast<float*>(s_b);  // [quarter][channel]
+    if (vcent != nullptr) {
+        const int cp = tid & 63, qq = tid >> 6;
+        const uint32_t* vc = reinterpret_cast<const uint32_t*>(s_vc) + cp;
+        float f0 = 0.0f, f1 = 0.0f;
+        for (int c = qq; c < vnc; c += 4) {
+            const uint32_t w = vc[c * (kDim / 2)];
+            f0 = fmaf(s_beta[c], h2f((uint16_t)(w & 0xFFFFu)), f0);
+            f1 = fmaf(s_beta[c], h2f((uint16_t)(w >> 16)), f1);
+        }
+        s_f[qq * kDim + 2 * cp] = f0;
+        s_f[qq * kDim + 2 * cp + 1] = f1;
+        __syncthreads();
+    }
+    // normalise (threads 0..127: one channel each)
     uint16_t oc = 0;
     if (tid < kDim) {
         const float* sd = reinterpret_cast<const float*>(s_d);
         float acc = 0.0f;
 #pragma unroll
         for (int g2 = 0; g2 < 8; ++g2) acc += sd[g2 * kDim + tid];
-        if (vcent != nullptr) {
-            const uint16_t* vc = reinterpret_cast<const uint16_t*>(s_vc) + tid;
-            for (int c = 0; c < vnc; ++c) acc = fmaf(s_beta[c], h2f(vc[c * kDim]), acc);
-        }
+        if (vcent != nullptr) acc += (s_f[tid] + s_f[kDim + tid]) + (s_f[2 * kDim + tid] + s_f[3 * kDim + tid]);
         const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
         oc = f2h(acc * inv);
         if constexpr (!RECENT) {
@@ -1582,7 +1619,7 @@ PartialLds partial_lds(int kf, const DTensor& k, int vf, const DTensor& v, int G
     const int merge_bytes = kWaves * G * kPartStride * 4;
     const int cent_bytes = kf != D_DENSE ? k.nc * kCPitch * 2 : 0;
     L.lut_off = cent_bytes > merge_bytes ? cent_bytes : merge_bytes;
-    L.p_off = L.lut_off + (kLutWords + kStructLutWords) * 4;
+    L.p_off = L.lut_off + (kLutWords + kStructLutWords + kQTrigWords) * 4;
     L.stage_off = L.p_off + kWaves * (kTile * G + kTile * kVPitch) * 2;
     L.bytes = (size_t)L.stage_off + (size_t)kWaves * (L.stage_k + L.stage_v);
     return L;
