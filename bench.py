@@ -297,7 +297,7 @@ def measure_quantized(torch, device, steps, layers=32):
     out = {}
     for bits in (4, 2):
         r = measure_point_bits(torch, 8, 16384, bits, layers, steps, device)
-        out[f"int{bits}"] = {k: r[k] for k in ("us_per_layer_step", "achieved_GBps", "frac", "splits")}
+        out[f"int{bits}"] = r
     return out
 
 
@@ -336,8 +336,13 @@ def measure_point_bits(torch, b, t, bits, layers, steps, device):
     nsplit = decode_splits(caches[0], HQ)
     del caches
     torch.cuda.empty_cache()
+    frac = nbytes / per_call / HBM_PEAK
+    rec = counter_record(b, t, 0.5, "unstructured", bits)
+    traffic, source = measured_traffic(rec, nsplit)
     return {"us_per_layer_step": per_call * 1e6, "achieved_GBps": nbytes / per_call / 1e9,
-            "frac": nbytes / per_call / HBM_PEAK, "splits": nsplit}
+            "frac": frac, "splits": nsplit, "bytes_per_call": nbytes, "traffic": traffic,
+            "traffic_ratio": traffic / nbytes if traffic else None, "traffic_source": source,
+            "ceiling": issue_ceiling(rec, nbytes, frac)}
 
 
 def measure_e2e(torch, device, batch=16, prompt=8192, steps=2048, warmup=4, attn_steps=8):
@@ -547,29 +552,53 @@ def copy_bandwidth(torch, device, nbytes=1 << 30, reps=10):
     return 2.0 * nbytes * reps / secs / 1e9
 
 
-def measured_traffic(b, t, sparsity, layout, splits):
-    """(HBM bytes per launch of the partial kernel, where that figure comes from)
-    from the committed rocprof run if it is this workload, else (None, None).
+def counter_record(b, t, sparsity, layout, bits=16):
+    """The committed rocprofv3 record of this workload's partial kernel
+    (profiles/decode_traffic.json), or None.
 
-    The figure comes from two rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE),
-    each scaled by what the same counter reads for a device copy of known
-    size; profiles/decode_partial_b32_s50.md holds the runs and the commands.
-    It is not measured by this run: the source names the profile, the split
-    count it was measured at and whether that is this run's split count.
+    Each record holds the HBM bytes per launch from two rocprofv3 --pmc passes
+    (FETCH_SIZE, WRITE_SIZE), each scaled by what the same counter reads for a
+    device copy of known size, and the instructions per (token, KV-head) from
+    three passes of SQ counters; the profiles under profiles/ hold the runs
+    and their commands.  None of it is measured by this run.
     """
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "decode_traffic.json")
     try:
         with open(path) as f:
             rec = json.load(f)
     except (OSError, ValueError):
+        return None
+    for w in rec.get("workloads", []):
+        if (w.get("batch"), w.get("seq_len"), w.get("sparsity"), w.get("layout"), w.get("bits")) == \
+                (b, t, sparsity, layout, bits):
+            return dict(w, clock_ghz=rec.get("clock_ghz"), source=rec.get("source"))
+    return None
+
+
+def measured_traffic(rec, splits):
+    """(HBM bytes per launch, where that figure comes from) from a counter record."""
+    if rec is None:
         return None, None
-    w = rec.get("workload", {})
-    if (w.get("batch"), w.get("seq_len"), w.get("sparsity"), w.get("layout")) != (b, t, sparsity, layout):
-        return None, None
-    source = {"profile": rec.get("source"), "file": "profiles/decode_traffic.json",
-              "measured_at_splits": w.get("splits"), "this_run_splits": splits,
+    source = {"profile": rec["source"], "file": "profiles/decode_traffic.json",
+              "measured_at_splits": rec["splits"], "this_run_splits": splits,
               "note": "copied from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE passes, not measured by this run"}
-    return (rec["fetch_bytes"] + rec["write_bytes"]) * 1000, source
+    return rec["fetch_bytes"] + rec["write_bytes"], source
+
+
+def issue_ceiling(rec, bytes_per_call, frac):
+    """The bandwidth fraction at which the partial kernel's vector ALU would be
+    busy every cycle with the instructions it issues per (token, KV-head) --
+    four SIMD cycles per wave64 VALU instruction, 1024 SIMDs at the recorded
+    shader clock -- and the measured fraction of that ceiling."""
+    if rec is None:
+        return None
+    cycles = 4.0 * rec["valu_per_unit"]
+    seconds = rec["units"] * cycles / (1024 * rec["clock_ghz"] * 1e9)
+    ceil = bytes_per_call / seconds / HBM_PEAK
+    return {"valu_per_unit": rec["valu_per_unit"], "mfma_per_unit": rec["mfma_per_unit"],
+            "valu_issue_ceiling_frac": ceil, "frac_of_ceiling": frac / ceil,
+            "basis": "VALU instructions per (token, KV-head) from the committed SQ counter passes "
+                     f"(profiles/decode_traffic.json), 4 cycles each, 1024 SIMDs at {rec['clock_ghz']} GHz"}
 
 
 def main():
@@ -637,7 +666,8 @@ def main():
         print(json.dumps({"e2e": e2e}), flush=True)
     copy_gbps = copy_bandwidth(torch, device)
     cpu = None if args.no_cpu_baseline else cpu_baseline()
-    traffic, traffic_source = measured_traffic(args.batch, args.seq_len, args.sparsity, r["layout"], r["splits"])
+    rec = counter_record(args.batch, args.seq_len, args.sparsity, r["layout"])
+    traffic, traffic_source = measured_traffic(rec, r["splits"])
     secs = r["seconds"]
     line = {
         "metric": METRIC,
@@ -678,6 +708,7 @@ def main():
         "roofline": {
             "bound": "hbm", "achieved": r["achieved_GBps"], "peak": HBM_PEAK / 1e9, "unit": "GB/s",
             "frac": r["frac"], "traffic": traffic, "traffic_source": traffic_source,
+            "ceiling": issue_ceiling(rec, r["bytes_per_call"], r["frac"]),
             "kernel": "one decode-attention call (decode_partial_kernel + decode_merge_kernel)",
             "bytes_per_call": r["bytes_per_call"],
             "copy_GBps": copy_gbps, "frac_of_copy": r["achieved_GBps"] / copy_gbps,

@@ -23,3 +23,36 @@ def test_metric_is_the_baseline_metric():
 
     baseline = json.loads((ROOT / "BASELINE.json").read_text())
     assert bench.METRIC == baseline["metric"]
+
+
+def test_counter_records_cover_the_bench_workloads():
+    """Every workload the line reports a roofline for has a committed counter
+    record: config 2 at both sparsities (B = 32) and config 3 at INT4 / INT2."""
+    sys.path.insert(0, str(ROOT))
+    import bench
+
+    for key in ((32, 8192, 0.5, "unstructured", 16), (32, 8192, 0.75, "structured", 16),
+                (8, 16384, 0.5, "unstructured", 4), (8, 16384, 0.5, "unstructured", 2)):
+        rec = bench.counter_record(*key)
+        assert rec is not None, key
+        assert rec["fetch_bytes"] > 0 and rec["units"] == key[0] * 8 * key[1]
+        traffic, source = bench.measured_traffic(rec, rec["splits"])
+        assert traffic == rec["fetch_bytes"] + rec["write_bytes"]
+        assert source["measured_at_splits"] == source["this_run_splits"]
+    assert bench.counter_record(32, 8192, 0.5, "unstructured", 4) is None
+    assert bench.measured_traffic(None, 2) == (None, None) and bench.issue_ceiling(None, 1, 0.1) is None
+
+
+def test_issue_ceiling_arithmetic():
+    """A kernel issuing V VALU instructions per unit on 1024 SIMDs at f GHz
+    spends 4 V / (1024 f) ns per unit; the ceiling is the bandwidth at that rate."""
+    sys.path.insert(0, str(ROOT))
+    import bench
+
+    rec = {"valu_per_unit": 20.0, "mfma_per_unit": 2.0, "units": 1 << 20, "clock_ghz": 2.0}
+    nbytes = 100 * (1 << 20)  # 100 B per unit
+    c = bench.issue_ceiling(rec, nbytes, 0.25)
+    seconds = (1 << 20) * 80 / (1024 * 2.0e9)
+    assert abs(c["valu_issue_ceiling_frac"] - nbytes / seconds / 8.0e12) < 1e-12
+    assert abs(c["valu_issue_ceiling_frac"] - 0.32) < 1e-12  # 100 B per 80 / (1024 * 2 GHz) s = 2.56 TB/s
+    assert abs(c["frac_of_ceiling"] - 0.25 / 0.32) < 1e-12
