@@ -383,3 +383,30 @@ def test_recent_window_longer_than_one_chunk(device, tr):
     out = attention(q, cache, position=pos, inv_freq=freq, recent=(qr, kr, vr))
     ref = expected_attention(q, cache, position=pos, inv_freq=freq, recent=(qr, kr, vr))
     assert _max_err(out, ref) <= ATOL
+
+
+@pytest.mark.parametrize("sparsity,layout", [(0.5, "unstructured"), (0.75, "structured")])
+def test_rope_table_growth_across_calls(device, sparsity, layout):
+    """One frequency set decoded at compressed positions that cross the RoPE
+    table's growth points (1,024 -> 2,048 -> 4,096 positions), then back down:
+    every call reads the table rows of its own positions, the grown table
+    replaces the old one and the old one stays alive, and each output matches
+    the float64 oracle at those positions."""
+    import reskv_amd._extension as ext
+
+    k, v, q = outlier_kv(1, 2, 700, seed=21, gqa=4)
+    cache = compress(k, v, ResKVKernelConfig(sparsity=sparsity, layout=layout, num_clusters=16))
+    # a frequency set no other test (or case) uses, so its table starts at
+    # 1,024 positions: the cache is per process
+    freq = theta_freq(123457.0 if sparsity == 0.5 else 223457.0)
+    before = len(ext._RETIRED)
+    sizes = []
+    for start in (300, 330, 1400, 3300, 20):
+        position = start + 700 + 3
+        out = attention(q, cache, position=position, start_position=start, inv_freq=freq)
+        ref = expected_attention(q, cache, position=position, start_position=start, inv_freq=freq)
+        assert float(np.abs(np_(out).astype(np.float64) - ref).max()) <= ATOL, start
+        key = ext._content_key(freq, freq.device)
+        sizes.append(ext._ROPE_TABLES[key][0].shape[0])
+    assert sizes == [1024, 2048, 4096, 4096, 4096]
+    assert len(ext._RETIRED) - before == 2
