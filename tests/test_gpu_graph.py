@@ -51,3 +51,43 @@ def test_graph_replays_equal_the_eager_call(device, bits, sparsity, layout):
         q.copy_(saved_q)
         torch.cuda.synchronize()
     del graph
+
+
+def test_graph_replays_of_the_prefill_compressor(device):
+    """K-means of K and V together and the K+V encoders, captured as bench.py
+    times them: every replay's centres, ids, payloads and metadata equal the
+    eager call's (the kernels are deterministic)."""
+    from reskv_amd._extension import load_extension
+    from reskv_amd.compression import cluster_kv
+
+    ext = load_extension("compression")
+    k, v, _ = outlier_kv(1, 4, 1500, seed=33, gqa=4)
+    (kc, ki), (vc, vi) = cluster_kv(k, v, 16, 5)
+    steps = {
+        "kmeans": lambda: cluster_kv(k, v, 16, 5),
+        "tile4": lambda: ext.compress_fp16_kv(k, kc, ki, v, vc, vi, 32, True),
+        "bitmap": lambda: ext.compress_bitmap_kv(k, kc, ki, v, vc, vi, 64),
+    }
+
+    def flat(x):
+        return [y for z in x for y in (flat(z) if isinstance(z, (tuple, list)) else [z])]
+
+    for name, fn in steps.items():
+        eager = [t.clone() for t in flat(fn())]
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            fn()
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            out = flat(fn())
+        assert len(out) == len(eager) > 0
+        for replay in range(3):
+            graph.replay()
+            torch.cuda.synchronize()
+            for a, b in zip(out, eager):
+                assert torch.equal(a, b), (name, replay)
+            fn()  # eager work between replays
+            torch.cuda.synchronize()
+        del graph
