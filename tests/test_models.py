@@ -83,6 +83,53 @@ def test_forward_checks():
             model(ids[:, :2], past_key_values=cache)
 
 
+@pytest.mark.parametrize("field", ["position_ids", "cache_position"])
+@pytest.mark.parametrize("phase", ["prefill", "decode"])
+def test_noncontiguous_positions_are_rejected(field, phase):
+    """Positions that skip one, given either way and in either phase, are
+    rejected (reskv tests/test_model.py:70-86)."""
+    model = ResKVForCausalLM(_config(), ResKVKernelConfig()).eval()
+    x = torch.randint(5, 300, (1, 16), generator=torch.Generator().manual_seed(2))
+    cache, start = None, 0
+    with torch.no_grad():
+        if phase == "decode":
+            cache = model(x).past_key_values
+            start = x.shape[-1]
+            x = x[:, :1]
+        positions = torch.arange(start, start + x.shape[-1]) + 1
+        if field == "position_ids":
+            positions = positions.unsqueeze(0)
+        with pytest.raises(ValueError, match="contiguous"):
+            model(x, past_key_values=cache, **{field: positions})
+
+
+def test_decode_padding_is_rejected():
+    """A decode step whose mask pads the history is rejected (reskv tests/test_model.py:89-97)."""
+    model = ResKVForCausalLM(_config(), ResKVKernelConfig()).eval()
+    x = torch.randint(5, 300, (1, 16), generator=torch.Generator().manual_seed(3))
+    with torch.no_grad():
+        cache = model(x).past_key_values
+        mask = torch.ones(1, 17, dtype=torch.long)
+        mask[:, 0] = 0
+        with pytest.raises(ValueError, match="unpadded"):
+            model(x[:, :1], past_key_values=cache, attention_mask=mask)
+
+
+def test_full_and_indexed_logits_keep_transformers_semantics():
+    """logits_to_keep: the default keeps the last position, 0 keeps all and a
+    tensor keeps the positions it names (reskv tests/test_model.py:100-109)."""
+    torch.manual_seed(4)
+    model = ResKVForCausalLM(_config(), ResKVKernelConfig()).eval()
+    x = torch.randint(5, 300, (1, 20), generator=torch.Generator().manual_seed(5))
+    with torch.no_grad():
+        last = model(x).logits
+        full = model(x, logits_to_keep=0).logits
+        selected = model(x, logits_to_keep=torch.tensor([0, 19])).logits
+    assert last.shape == (1, 1, 300) and full.shape == (1, 20, 300) and selected.shape == (1, 2, 300)
+    torch.testing.assert_close(last, full[:, -1:])
+    torch.testing.assert_close(selected, full[:, [0, 19]])
+
+
 def test_from_pretrained_takes_the_kernel_config(tmp_path):
     """transformers 5 reserves ``kernel_config`` in from_pretrained; the ResKV settings still arrive."""
     LlamaForCausalLM(_config()).save_pretrained(tmp_path)
