@@ -126,3 +126,31 @@ def test_encoder_rejects_bad_inputs(ext, device):
         ext.compress_bitmap(x.float(), c, ids, 32)
     with pytest.raises(RuntimeError, match="identical shapes"):
         ext.compress_bitmap_kv(x, c, ids, x[:, :, :2].contiguous(), c, ids[:, :, :2].contiguous(), 32)
+
+
+def test_layouts_have_different_selection_semantics(device):
+    """75% unstructured and 75% structured keep the same number of values per
+    token (32) but select different ones: global top-32 against the top 4 of
+    every 16-channel tile (reskv tests/test_cuda.py:92-97).  (The bit-exact
+    checks of each encoder against its oracle are the tests above.)"""
+    from reskv_amd import ResKVKernelConfig, compress
+    from tests.gpu_helpers import dense, reference_test_inputs
+
+    k, v, _, c = reference_test_inputs(t=64)
+    u = compress(k, v, ResKVKernelConfig(bits=16, sparsity=0.75, layout="unstructured"), clustering=c)
+    s = compress(k, v, ResKVKernelConfig(bits=16, sparsity=0.75, layout="structured"), clustering=c)
+    assert u.key.payload.shape[-1] == s.key.payload.shape[-1] == 32
+    du, ds = dense(u.key), dense(s.key)
+    assert not np.array_equal(du, ds)
+    # every structured tile keeps exactly four channels; the unstructured rows do not
+    kept_s = (ds - dense_centroids(s.key)) != 0
+    kept_u = (du - dense_centroids(u.key)) != 0
+    assert (kept_s.reshape(*kept_s.shape[:-1], 8, 16).sum(-1) <= 4).all()
+    assert (kept_u.reshape(*kept_u.shape[:-1], 8, 16).sum(-1) > 4).any()
+
+
+def dense_centroids(ct):
+    """Each token's centroid row (float64 [B, H, T, 128])."""
+    cent = np_(ct.centroids).astype(np.float64)
+    ids = np_(ct.cluster_ids).astype(np.int64)
+    return np.take_along_axis(cent, ids[..., None].repeat(128, -1), axis=2)
