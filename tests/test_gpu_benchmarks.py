@@ -24,6 +24,34 @@ def test_kernel_sweep_writes_checked_records(device, tmp_path, monkeypatch):
         assert record["decode_ms"] > 0 and record["compression_ms"] > 0 and record["cache_bytes"] > 0
 
 
+def test_kernel_sweep_releases_previous_case(device, tmp_path, monkeypatch):
+    """Each case's inputs and compressed payloads are released before the next
+    case allocates its own (reskv tests/test_benchmark.py:17-45)."""
+    import weakref
+
+    from reskv_amd.benchmarks import kernels
+
+    tracked = []
+    original_inputs, original_compress = kernels._inputs, kernels.compress
+
+    def inputs(*args, **kwargs):
+        assert all(ref() is None for ref in tracked)
+        return original_inputs(*args, **kwargs)
+
+    def compress(*args, **kwargs):
+        cache = original_compress(*args, **kwargs)
+        tracked.extend(weakref.ref(x) for x in (*args[:2], cache.key.payload, cache.value.payload))
+        return cache
+
+    monkeypatch.setattr(kernels, "_inputs", inputs)
+    monkeypatch.setattr(kernels, "compress", compress)
+    monkeypatch.setattr(kernels, "median_event_ms", lambda fn: 0.0)
+    monkeypatch.setattr(sys, "argv", ["kernels", "--batch-sizes", "1", "2", "--seq-len", "128", "--output",
+                                      str(tmp_path / "kernels.json")])
+    kernels.main()
+    assert tracked and all(ref() is None for ref in tracked)
+
+
 def test_kernel_sweep_against_the_fp32_checker(device):
     """The sweep's own inputs and caches, checked by the float32 port of the oracle."""
     from oracle import torch_checker
