@@ -130,6 +130,65 @@ def test_full_and_indexed_logits_keep_transformers_semantics():
     torch.testing.assert_close(selected, full[:, [0, 19]])
 
 
+def _small():
+    return LlamaConfig(hidden_size=256, intermediate_size=512, num_hidden_layers=1, num_attention_heads=2,
+                       num_key_value_heads=2, vocab_size=32)
+
+
+def test_kernel_config_round_trips_through_checkpoint(tmp_path):
+    """Settings stored in the model config build the model and survive
+    save/reload (reskv tests/test_config.py:148-174)."""
+    settings = ResKVKernelConfig(sparsity=0.75, bits=4, num_clusters=4, max_clusters=8, rope_mode="theta")
+    config = _small()
+    config.reskv_kernel_config = settings.to_dict()
+    model = ResKVForCausalLM(config).eval()
+    assert model.kernel_config == settings
+    model.save_pretrained(tmp_path)
+    assert ResKVForCausalLM.from_pretrained(tmp_path).kernel_config == settings
+
+
+def test_model_rejects_configuration_of_another_kind():
+    """A kernel_config of another type is a TypeError; stored settings that are
+    not this class's are not silently reinterpreted; an explicit configuration
+    still reuses the checkpoint (reskv tests/test_config.py:177-205)."""
+    config = _small()
+    with pytest.raises(TypeError, match="expected ResKVKernelConfig"):
+        ResKVForCausalLM(config, kernel_config={"sparsity": 0.5})
+    config.reskv_kernel_config = {"sparsity": 0.5, "bits": 16, "residual_mode": "topk"}  # another method's fields
+    with pytest.raises(ValueError, match="checkpoint compression settings"):
+        ResKVForCausalLM(config)
+    model = ResKVForCausalLM(config, kernel_config=ResKVKernelConfig())
+    assert model.kernel_config == ResKVKernelConfig()
+
+
+@pytest.mark.parametrize("stored", [False, 0, "", []])
+def test_invalid_stored_settings_are_not_replaced_with_defaults(stored):
+    """(reskv tests/test_config.py:234-241)"""
+    config = _small()
+    config.reskv_kernel_config = stored
+    with pytest.raises(ValueError, match="checkpoint compression settings"):
+        ResKVForCausalLM(config)
+
+
+def test_model_rejects_configuration_of_another_architecture():
+    """(reskv tests/test_config.py:214-224)"""
+    from transformers import Qwen3Config
+
+    with pytest.raises(ValueError, match="configuration"):
+        ResKVForCausalLM(Qwen3Config())
+
+
+def test_public_functions_survive_model_import_order():
+    """Importing the model (which imports the attention module) does not shadow
+    the public callables (reskv tests/test_config.py:244-255)."""
+    import subprocess
+    import sys
+
+    subprocess.run([sys.executable, "-c", "from reskv_amd import ResKVForCausalLM; "
+                    "from reskv_amd import attention, compress; assert callable(attention) and callable(compress)"],
+                   check=True, timeout=300)
+
+
 def test_from_pretrained_takes_the_kernel_config(tmp_path):
     """transformers 5 reserves ``kernel_config`` in from_pretrained; the ResKV settings still arrive."""
     LlamaForCausalLM(_config()).save_pretrained(tmp_path)
