@@ -122,3 +122,26 @@ def test_emulation_catches_a_coarser_weight_rounding():
     pb = bf16(p)
     coarse = np.abs(np.einsum("rt,rtd->rd", pb / pb.sum(1, keepdims=True), v) - exact).max()
     assert coarse > 4 * fine
+
+
+def test_fp16_scores_would_exceed_the_tolerance_at_config3():
+    """Why the scores stay on fp32 matrix cores.  An fp16 score product would
+    round the rotated key and the rotated, pre-scaled query to fp16.  On the
+    config-2 inputs that moves the output by a few 1e-6; on config 3's
+    outlier-channel keys (scores up to ~20) the score errors reach ~0.01 and
+    the output error passes the 2e-3 tolerance."""
+    freq = o.theta_frequencies(500000.0)
+
+    def f16(x):
+        return x.astype(np.float16).astype(np.float64)
+
+    errs = {}
+    for config, seed in ((2, 1), (3, 2)):
+        q, k, v, t = _inputs(config, np.random.default_rng(seed), rows=8)
+        qr = o.rotate(q, np.array([t]), freq) * 128 ** -0.5
+        kr = o.rotate(k, np.arange(t), freq)
+        s = np.einsum("rd,rtd->rt", qr, kr)
+        s16 = np.einsum("rd,rtd->rt", f16(qr), f16(kr))
+        errs[config] = np.abs(exact_average(s16, v) - exact_average(s, v)).max()
+    assert errs[2] < 1e-4, errs  # measured 3.2e-6
+    assert errs[3] > 2e-3, errs  # measured 2.95e-3
